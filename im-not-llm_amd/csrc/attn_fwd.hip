@@ -1,0 +1,712 @@
+// Packed variable-length encoder attention for MI355X (gfx950).
+//
+// One kernel template serves every attention form of the encoder engines
+// (causal GQA, bidirectional full, sliding window): a query i of a text sees
+// key j of the same text iff (!causal || j <= i) && (window < 0 ||
+// |i - j| <= window). It replaces the reference's padded attention calls
+// (crates/inl-core/src/attention.rs:215-315, crates/inl-text/src/gemma2.rs:
+// 414-441, crates/inl-sparse/src/modernbert.rs:366-401,
+// crates/inl-late/src/qwen3_5.rs:364-407, crates/inl-vision/src/vision.rs:
+// 226-259) with one launch per layer over packed texts.
+//
+// Work decomposition. The host builds a tile schedule: one item per
+// (text, block of BLOCK_M query rows) holding the range of BLOCK_N-key tiles
+// the rows can see (tiles above the causal diagonal, outside the window or in
+// other texts are never visited), sorted by cost, longest first. A workgroup
+// takes one item for `hpw` query heads that share one KV head, so every K/V
+// tile staged in LDS serves hpw * BLOCK_M query rows. Each 64-lane wave owns
+// 32 query rows of one head.
+//
+// Per wave and key tile (32x32 MFMA tiles, fp32 accumulation):
+//   S^T[key, query] = K . Q^T      A = K rows from LDS, B = Q^T in registers
+//   online softmax on S^T columns  (each lane owns one query; the max needs a
+//                                   single cross-half exchange, the row sum is
+//                                   combined once at the end)
+//   O^T[d, query] += V^T . P^T     A = V^T from LDS, B = P^T from registers
+// Computing the transposed products keeps every query's scores and output in
+// its own lane, so softmax rescaling is lane-local. V is transposed while it
+// is staged into LDS (register transposes of 4-key groups), and its key
+// columns are stored in the order the S^T accumulator hands P to the PV
+// product, so P never moves between lanes.
+//
+// bf16 inputs: QK^T on v_mfma_f32_32x32x16_bf16. For PV, V is converted to
+// fp16 while it is staged (exact for every bf16 value of magnitude below
+// 65504) and P is rounded to fp16, so PV runs on v_mfma_f32_32x32x16_f16 with
+// 8x the P precision of bf16: a causal row that sees two keys of comparable
+// weight would otherwise carry up to ~4e-3 of P rounding error. The flag
+// INL_ATTN_PV_BF16 keeps V and P in bf16 instead (any V range, coarser P).
+// f32 inputs use v_mfma_f32_32x32x2_f32 throughout.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "inl_common.hpp"
+
+namespace inl {
+
+namespace {
+
+struct AttnParams {
+  const char* q;
+  const char* k;
+  const char* v;
+  char* o;
+  int64_t q_stride, k_stride, v_stride, o_stride;  // elements between token rows
+  const int4* items;  // {seg_start, seg_len, q0, (lo_tile << 16) | hi_tile}
+  int32_t n_hg;       // workgroups per item
+  int32_t groups_per_kv;  // (h_q / h_kv) / hpw
+  int32_t group;      // h_q / h_kv
+  int32_t hpw;        // query heads per workgroup
+  int32_t rb;         // 32-row blocks per head per workgroup (NW / hpw)
+  int32_t head_dim;
+  int32_t causal;
+  int32_t window;
+  float scale_log2;   // scale * log2(e)
+  int32_t out_bf16;
+};
+
+// Element type of V^T in LDS and of P for the PV product.
+template <typename E, bool PV16>
+struct PvType { typedef float T; };
+template <> struct PvType<bf16, true> { typedef f16 T; };
+template <> struct PvType<bf16, false> { typedef bf16 T; };
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float wave_xor32(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+// Byte offset of 16-byte chunk `c` of row `r` in a row-major tile whose rows
+// are `row_bytes` long. The XOR keeps the 8 rows a group of lanes reads at
+// one logical chunk in 8 distinct chunk columns (bank-conflict free).
+__device__ __forceinline__ int swz(int r, int c, int row_bytes) {
+  return r * row_bytes + ((c ^ (r & 7)) << 4);
+}
+
+// Column of a 4-key group inside a V^T row. bf16: within 16 keys, swap key
+// bits 2 and 3, so lane-half h of the PV product reads its 8 keys
+// {8a + 4h + b} (a, b the S^T accumulator's row split) as one 16-byte chunk.
+// f32: within 32 keys, key 8a + 4h + b goes to 16h + 4a + b.
+template <typename E>
+__device__ __forceinline__ int vcol(int key4) {
+  if constexpr (sizeof(E) == 2) {
+    return (key4 & ~15) | ((key4 & 4) << 1) | ((key4 & 8) >> 1);
+  } else {
+    return (key4 & ~31) | ((key4 & 4) << 2) | ((key4 & 24) >> 1);
+  }
+}
+
+template <typename E, int D, int BN, int NW, bool PV16>
+__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
+  typedef typename PvType<E, PV16>::T PT;
+  constexpr int NT = NW * 64;
+  constexpr int ES = (int)sizeof(E);
+  constexpr int VEC = 16 / ES;          // elements per 16-byte chunk
+  constexpr int CHK = D / VEC;          // chunks per K row
+  constexpr int KROW = D * ES;          // bytes per K row in LDS
+  constexpr int VROW = BN * ES;         // bytes per V^T row in LDS
+  constexpr int KT_BYTES = BN * D * ES; // one K (or V^T) tile
+  constexpr int NKC = BN * CHK;         // K chunks per tile
+  constexpr int NVU = (BN / 4) * CHK;   // V units (4 keys x 1 chunk) per tile
+  constexpr int KPT = (NKC + NT - 1) / NT;
+  constexpr int VPT = (NVU + NT - 1) / NT;
+  constexpr int NKB = BN / 32;          // 32-key blocks per tile
+  constexpr int NDB = D / 32;           // 32-wide d blocks of the output
+  static_assert(CHK >= 8 && (VROW / 16) >= 8, "swizzle needs 8 chunks per row");
+  static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
+
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lq = lane & 31;   // query column this lane owns
+  const int hf = lane >> 5;   // lane half
+
+  const int item_idx = blockIdx.x / p.n_hg;
+  const int hg = blockIdx.x - item_idx * p.n_hg;
+  const int4 it = p.items[item_idx];
+  const int seg = it.x;
+  const int T = it.y;
+  const int q0 = it.z;
+  const int lo_t = it.w >> 16;
+  const int hi_t = it.w & 0xffff;
+  const int kvh = hg / p.groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + wave / p.rb;
+  const int r0 = q0 + (wave % p.rb) * 32;  // first query row of this wave
+  const int hd = p.head_dim;
+  const bool active = r0 < T;
+
+  // Key range this wave can see (text-local, [klo, khi)).
+  const int rlast = min(r0 + 31, T - 1);
+  int klo = 0, khi = p.causal ? min(T, r0 + 32) : T;
+  if (p.window >= 0) {
+    klo = max(0, r0 - p.window);
+    khi = min(khi, rlast + p.window + 1);
+  }
+
+  // ---- Q^T operand, resident in registers for the whole item ----
+  const int qrow = r0 + lq;
+  const bool qvalid = qrow < T;
+  const char* qptr = p.q + ((int64_t)(seg + (qvalid ? qrow : 0)) * p.q_stride + (int64_t)head * hd) * ES;
+  constexpr int QC = D / VEC / 2;  // chunks of Q per lane
+  u32x4 qreg[QC];
+#pragma unroll
+  for (int i = 0; i < QC; ++i) {
+    const int c = 2 * i + hf;  // 16-byte chunk of the row
+    u32x4 z = {0u, 0u, 0u, 0u};
+    if (qvalid && c * VEC < hd) z = *reinterpret_cast<const u32x4*>(qptr + c * 16);
+    qreg[i] = z;
+  }
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[i][r] = 0.f;
+  float m_i = -INFINITY;
+  float l_i = 0.f;
+
+  // ---- staging of one K/V tile: global -> registers -> LDS ----
+  u32x4 kst[KPT];
+  u32x4 vst[VPT][4];
+  const char* kbase = p.k + ((int64_t)seg * p.k_stride + (int64_t)kvh * hd) * ES;
+  const char* vbase = p.v + ((int64_t)seg * p.v_stride + (int64_t)kvh * hd) * ES;
+
+  auto load_tile = [&](int t) {
+    const int kt0 = t * BN;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int id = tid + i * NT;
+      u32x4 z = {0u, 0u, 0u, 0u};
+      if (NKC % NT == 0 || id < NKC) {
+        const int row = id / CHK, c = id % CHK;
+        const int key = kt0 + row;
+        if (key < T && c * VEC < hd)
+          z = *reinterpret_cast<const u32x4*>(kbase + ((int64_t)key * p.k_stride) * ES + c * 16);
+      }
+      kst[i] = z;
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int id = tid + i * NT;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x4 z = {0u, 0u, 0u, 0u};
+        if (NVU % NT == 0 || id < NVU) {
+          const int g = id / CHK, c = id % CHK;
+          const int key = kt0 + 4 * g + j;
+          if (key < T && c * VEC < hd)
+            z = *reinterpret_cast<const u32x4*>(vbase + ((int64_t)key * p.v_stride) * ES + c * 16);
+        }
+        vst[i][j] = z;
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    char* sK = smem + buf * 2 * KT_BYTES;
+    char* sV = sK + KT_BYTES;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int id = tid + i * NT;
+      if (NKC % NT == 0 || id < NKC) {
+        const int row = id / CHK, c = id % CHK;
+        *reinterpret_cast<u32x4*>(sK + swz(row, c, KROW)) = kst[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int id = tid + i * NT;
+      if (NVU % NT == 0 || id < NVU) {
+        const int g = id / CHK, c = id % CHK;
+        const int col = vcol<E>(4 * g);  // key column of this 4-key group
+        if constexpr (ES == 2) {
+          // 4 keys x 8 d (bf16) -> for each d, 4 consecutive keys (8 bytes)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int w = e >> 1;
+            uint32_t a0 = vst[i][0][w], a1 = vst[i][1][w], a2 = vst[i][2][w], a3 = vst[i][3][w];
+            uint32_t lo, hi;
+            if constexpr (PV16) {
+              // bf16 -> f32 (bit shift) -> fp16 (RNE; exact below 65504)
+              auto f = [&](uint32_t x) { return __builtin_bit_cast(float, (e & 1) ? (x & 0xffff0000u) : (x << 16)); };
+              f32x2 x01 = {f(a0), f(a1)}, x23 = {f(a2), f(a3)};
+              lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(x01, f16x2));
+              hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(x23, f16x2));
+            } else if (e & 1) {
+              lo = (a0 >> 16) | (a1 & 0xffff0000u);
+              hi = (a2 >> 16) | (a3 & 0xffff0000u);
+            } else {
+              lo = (a0 & 0xffffu) | (a1 << 16);
+              hi = (a2 & 0xffffu) | (a3 << 16);
+            }
+            const int dd = c * 8 + e;
+            u32x2 val = {lo, hi};
+            *reinterpret_cast<u32x2*>(sV + swz(dd, col >> 3, VROW) + (col & 7) * 2) = val;
+          }
+        } else {
+          // 4 keys x 4 d (f32) -> for each d, 4 consecutive keys (16 bytes)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int dd = c * 4 + e;
+            u32x4 val = {vst[i][0][e], vst[i][1][e], vst[i][2][e], vst[i][3][e]};
+            *reinterpret_cast<u32x4*>(sV + swz(dd, col >> 2, VROW)) = val;
+          }
+        }
+      }
+    }
+  };
+
+  if (lo_t < hi_t) {
+    load_tile(lo_t);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  const float c2 = p.scale_log2;
+
+  for (int t = lo_t; t < hi_t; ++t) {
+    const int buf = (t - lo_t) & 1;
+    const bool more = t + 1 < hi_t;
+    if (more) load_tile(t + 1);
+
+    const int kt0 = t * BN;
+    if (active && kt0 < khi && kt0 + BN > klo) {
+      const char* sK = smem + buf * 2 * KT_BYTES;
+      const char* sV = sK + KT_BYTES;
+
+      // ---- S^T = K . Q^T ----
+      f32x16 sacc[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+        const int krow = kb * 32 + lq;
+        if constexpr (ES == 2) {
+#pragma unroll
+          for (int st = 0; st < D / 16; ++st) {
+            if (st * 16 < hd) {
+              bf16x8 a = *reinterpret_cast<const bf16x8*>(sK + swz(krow, 2 * st + hf, KROW));
+              bf16x8 b = __builtin_bit_cast(bf16x8, qreg[st]);
+              sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, sacc[kb], 0, 0, 0);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int g = 0; g < D / 8; ++g) {
+            if (g * 8 < hd) {
+              f32x4 a = *reinterpret_cast<const f32x4*>(sK + swz(krow, 2 * g + hf, KROW));
+              f32x4 b = __builtin_bit_cast(f32x4, qreg[g]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], b[e], sacc[kb], 0, 0, 0);
+            }
+          }
+        }
+      }
+
+      // ---- mask (only tiles that cross an edge of the visible region) ----
+      const bool need_mask =
+          (kt0 + BN > T) || (p.causal && kt0 + BN - 1 > r0) ||
+          (p.window >= 0 && (rlast - kt0 > p.window || kt0 + BN - 1 - r0 > p.window));
+      if (need_mask) {
+        const int qi = r0 + lq;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int kj = kt0 + kb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            bool ok = kj < T;
+            if (p.causal) ok = ok && kj <= qi;
+            if (p.window >= 0) ok = ok && abs(qi - kj) <= p.window;
+            if (!ok) sacc[kb][r] = -INFINITY;
+          }
+      }
+
+      // ---- online softmax (log2 domain, f32) ----
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+      mx = fmaxf(mx, wave_xor32(mx));
+      const float m_new = fmaxf(m_i, mx * c2);
+      const float base = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_i - base);
+      m_i = m_new;
+      l_i *= alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          sacc[kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], c2, -base));
+
+      // ---- O^T += V^T . P^T ----
+      if constexpr (ES == 2) {
+        // P is rounded (fp16, or bf16 with INL_ATTN_PV_BF16) for the product;
+        // the row sum is taken over the same rounded values (dot2 against
+        // ones), so the weights that multiply V sum exactly to the normaliser.
+        typedef PT pt8 __attribute__((ext_vector_type(8)));
+        typedef PT pt2 __attribute__((ext_vector_type(2)));
+        pt8 pk[BN / 16];
+        const pt2 ones = {(PT)1.0f, (PT)1.0f};
+#pragma unroll
+        for (int ks = 0; ks < BN / 16; ++ks) {
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            f32x2 pr = {sacc[ks >> 1][8 * (ks & 1) + e], sacc[ks >> 1][8 * (ks & 1) + e + 1]};
+            pt2 pair = __builtin_convertvector(pr, pt2);
+            pk[ks][e] = pair[0];
+            pk[ks][e + 1] = pair[1];
+            if constexpr (PV16) l_i = __builtin_amdgcn_fdot2(pair, ones, l_i, false);
+            else l_i = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l_i, false);
+          }
+        }
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          if (db * 32 < hd) {
+            const int vrow = db * 32 + lq;
+#pragma unroll
+            for (int ks = 0; ks < BN / 16; ++ks) {
+              pt8 a = *reinterpret_cast<const pt8*>(sV + swz(vrow, 2 * ks + hf, VROW));
+              if constexpr (PV16)
+                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pk[ks], oacc[db], 0, 0, 0);
+              else
+                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[ks], oacc[db], 0, 0, 0);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) l_i += sacc[kb][r];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          if (db * 32 < hd) {
+            const int vrow = db * 32 + lq;
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+              for (int q4 = 0; q4 < 4; ++q4) {
+                f32x4 a = *reinterpret_cast<const f32x4*>(sV + swz(vrow, 8 * kb + 4 * hf + q4, VROW));
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], sacc[kb][4 * q4 + e], oacc[db], 0, 0, 0);
+              }
+            }
+          }
+        }
+      }
+    }
+
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: O = O^T / l, one query row per lane column ----
+  if (!active || !qvalid) return;
+  const float l_tot = l_i + wave_xor32(l_i);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  char* orow = p.o + ((int64_t)(seg + qrow) * p.o_stride + (int64_t)head * hd) * (p.out_bf16 ? 2 : 4);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = db * 32 + 8 * g + 4 * hf;
+      if (d0 < hd) {
+        if (p.out_bf16) {
+          bf16x4 val;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) val[e] = (bf16)(oacc[db][4 * g + e] * inv);
+          *reinterpret_cast<bf16x4*>(orow + d0 * 2) = val;
+        } else {
+          f32x4 val;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e] * inv;
+          *reinterpret_cast<f32x4*>(orow + d0 * 4) = val;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: kernel selection, schedule, launch
+// ---------------------------------------------------------------------------
+
+typedef void (*KernelFn)(AttnParams);
+
+struct KernelCfg {
+  KernelFn fn;
+  int d;        // compiled head dim (>= real head_dim)
+  int bn;       // keys per tile
+  int nw;       // waves per workgroup
+  int lds;      // dynamic LDS bytes
+};
+
+template <typename E, int D, int BN, int NW, bool PV16>
+KernelCfg make_cfg() {
+  return KernelCfg{attn_fwd_kernel<E, D, BN, NW, PV16>, D, BN, NW, 4 * BN * D * (int)sizeof(E)};
+}
+
+int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, KernelCfg* cfg) {
+  const bool pv16 = !(flags & INL_ATTN_PV_BF16);
+  if (dtype == INL_BF16) {
+    if (head_dim <= 64) *cfg = pv16 ? make_cfg<bf16, 64, 64, 4, true>() : make_cfg<bf16, 64, 64, 4, false>();
+    else if (head_dim <= 128) *cfg = pv16 ? make_cfg<bf16, 128, 64, 4, true>() : make_cfg<bf16, 128, 64, 4, false>();
+    else if (head_dim <= 256) *cfg = pv16 ? make_cfg<bf16, 256, 64, 4, true>() : make_cfg<bf16, 256, 64, 4, false>();
+    else return fail(INL_E_UNSUPPORTED, "attention: head_dim > 256 is not supported");
+  } else {
+    if (head_dim <= 64) *cfg = make_cfg<float, 64, 64, 4, false>();
+    else if (head_dim <= 128) *cfg = make_cfg<float, 128, 64, 4, false>();
+    else if (head_dim <= 256) *cfg = make_cfg<float, 256, 32, 4, false>();
+    else return fail(INL_E_UNSUPPORTED, "attention: head_dim > 256 is not supported");
+  }
+  return INL_OK;
+}
+
+// Largest divisor of `group` that also divides the wave count.
+int heads_per_wg(int group, int nw) {
+  for (int h = std::min(group, nw); h >= 1; --h)
+    if (group % h == 0 && nw % h == 0) return h;
+  return 1;
+}
+
+int validate_desc(const inl_attn_desc* d, int64_t* total_tokens) {
+  if (!d) return fail(INL_E_INVALID, "attention: desc is NULL");
+  if (!dtype_ok(d->dtype) || !dtype_ok(d->out_dtype))
+    return fail(INL_E_INVALID, "attention: dtype must be INL_F32 or INL_BF16");
+  if (d->h_q <= 0 || d->h_kv <= 0 || d->h_q % d->h_kv != 0)
+    return fail(INL_E_INVALID, "attention: h_q must be a positive multiple of h_kv");
+  if (d->head_dim < 8 || d->head_dim > 256 || d->head_dim % 8 != 0)
+    return fail(INL_E_UNSUPPORTED, "attention: head_dim must be a multiple of 8 in [8, 256]");
+  if (d->causal != 0 && d->causal != 1) return fail(INL_E_INVALID, "attention: causal must be 0 or 1");
+  if (d->window < -1) return fail(INL_E_INVALID, "attention: window must be -1 or >= 0");
+  if (d->flags & ~INL_ATTN_PV_BF16) return fail(INL_E_INVALID, "attention: unknown flags");
+  if (!(d->scale > 0.f) || !std::isfinite(d->scale))
+    return fail(INL_E_INVALID, "attention: scale must be finite and > 0");
+  const int es = dtype_size(d->dtype);
+  const int vec = 16 / es;
+  auto stride_ok = [&](int64_t s, int64_t minimum, int esz) {
+    return s >= minimum && (s * esz) % 16 == 0;
+  };
+  const int64_t qs = d->q_row_stride ? d->q_row_stride : (int64_t)d->h_q * d->head_dim;
+  const int64_t ks = d->k_row_stride ? d->k_row_stride : (int64_t)d->h_kv * d->head_dim;
+  const int64_t vs = d->v_row_stride ? d->v_row_stride : (int64_t)d->h_kv * d->head_dim;
+  const int64_t os = d->o_row_stride ? d->o_row_stride : (int64_t)d->h_q * d->head_dim;
+  (void)vec;
+  if (!stride_ok(qs, (int64_t)d->h_q * d->head_dim, es) ||
+      !stride_ok(ks, (int64_t)d->h_kv * d->head_dim, es) ||
+      !stride_ok(vs, (int64_t)d->h_kv * d->head_dim, es) ||
+      !stride_ok(os, (int64_t)d->h_q * d->head_dim, dtype_size(d->out_dtype)))
+    return fail(INL_E_INVALID,
+                "attention: row strides must cover all heads and be multiples of 16 bytes");
+  if (d->n_texts < 0) return fail(INL_E_INVALID, "attention: n_texts < 0");
+  if (d->n_texts > 0 && !d->cu_seqlens_host)
+    return fail(INL_E_INVALID, "attention: cu_seqlens_host is NULL");
+  int rc = check_cu(d->n_texts, d->cu_seqlens_host, total_tokens);
+  if (rc) return rc;
+  for (int b = 0; b < d->n_texts; ++b)
+    if (d->cu_seqlens_host[b + 1] - d->cu_seqlens_host[b] >= (1 << 16) * 32)
+      return fail(INL_E_UNSUPPORTED, "attention: a text longer than 2^21 tokens");
+  return INL_OK;
+}
+
+struct Schedule {
+  std::vector<int4> items;
+  int block_m = 0;
+  int hpw = 1;
+  KernelCfg cfg{};
+};
+
+int build_schedule(const inl_attn_desc* d, Schedule* s) {
+  int rc = select_kernel(d->dtype, d->head_dim, d->flags, &s->cfg);
+  if (rc) return rc;
+  const int group = d->h_q / d->h_kv;
+  s->hpw = heads_per_wg(group, s->cfg.nw);
+  s->block_m = 32 * (s->cfg.nw / s->hpw);
+  const int BM = s->block_m, BN = s->cfg.bn;
+  struct Tmp { int4 it; int cost; };
+  std::vector<Tmp> tmp;
+  for (int b = 0; b < d->n_texts; ++b) {
+    const int seg = d->cu_seqlens_host[b];
+    const int T = d->cu_seqlens_host[b + 1] - seg;
+    for (int q0 = 0; q0 < T; q0 += BM) {
+      const int qlast = std::min(q0 + BM, T) - 1;
+      int lo = 0, hi = d->causal ? qlast + 1 : T;
+      if (d->window >= 0) {
+        lo = std::max(0, q0 - d->window);
+        hi = std::min(hi, qlast + d->window + 1);
+      }
+      const int lo_t = lo / BN, hi_t = (hi + BN - 1) / BN;
+      tmp.push_back({make_int4(seg, T, q0, (lo_t << 16) | hi_t), hi_t - lo_t});
+    }
+  }
+  std::stable_sort(tmp.begin(), tmp.end(), [](const Tmp& a, const Tmp& b) { return a.cost > b.cost; });
+  s->items.resize(tmp.size());
+  for (size_t i = 0; i < tmp.size(); ++i) s->items[i] = tmp[i].it;
+  return INL_OK;
+}
+
+AttnParams make_params(const inl_attn_desc* d, const Schedule& s, const int4* items,
+                       const void* q, const void* k, const void* v, void* out) {
+  AttnParams p{};
+  p.q = (const char*)q;
+  p.k = (const char*)k;
+  p.v = (const char*)v;
+  p.o = (char*)out;
+  p.q_stride = d->q_row_stride ? d->q_row_stride : (int64_t)d->h_q * d->head_dim;
+  p.k_stride = d->k_row_stride ? d->k_row_stride : (int64_t)d->h_kv * d->head_dim;
+  p.v_stride = d->v_row_stride ? d->v_row_stride : (int64_t)d->h_kv * d->head_dim;
+  p.o_stride = d->o_row_stride ? d->o_row_stride : (int64_t)d->h_q * d->head_dim;
+  p.items = items;
+  p.group = d->h_q / d->h_kv;
+  p.hpw = s.hpw;
+  p.groups_per_kv = p.group / s.hpw;
+  p.n_hg = d->h_kv * p.groups_per_kv;
+  p.rb = s.cfg.nw / s.hpw;
+  p.head_dim = d->head_dim;
+  p.causal = d->causal;
+  p.window = d->window;
+  p.scale_log2 = d->scale * kLog2e;
+  p.out_bf16 = d->out_dtype == INL_BF16;
+  return p;
+}
+
+std::mutex g_attr_mu;
+
+int launch(const KernelCfg& cfg, const AttnParams& p, int64_t n_items, hipStream_t stream) {
+  if (n_items == 0) return INL_OK;
+  const int64_t blocks = n_items * p.n_hg;
+  if (blocks > 0x7fffffff) return fail(INL_E_UNSUPPORTED, "attention: too many tiles for one launch");
+  {
+    std::lock_guard<std::mutex> lock(g_attr_mu);
+    INL_HIP_TRY(hipFuncSetAttribute((const void*)cfg.fn, hipFuncAttributeMaxDynamicSharedMemorySize, cfg.lds));
+  }
+  hipLaunchKernelGGL(cfg.fn, dim3((unsigned)blocks), dim3(cfg.nw * 64), cfg.lds, stream, p);
+  INL_HIP_TRY(hipGetLastError());
+  return INL_OK;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+int check_ptrs(const void* q, const void* k, const void* v, const void* out, int64_t total) {
+  if (total == 0) return INL_OK;
+  if (!q || !k || !v || !out) return fail(INL_E_INVALID, "attention: NULL tensor pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(INL_E_INVALID, "attention: q, k, v and out must be 16-byte aligned");
+  return INL_OK;
+}
+
+}  // namespace
+
+}  // namespace inl
+
+struct inl_attn_plan {
+  inl_attn_desc desc;     // cu_seqlens_host is not kept
+  inl::Schedule sched;    // items also kept on the host for inspection
+  int4* d_items = nullptr;
+  int64_t total_tokens = 0;
+};
+
+extern "C" int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** plan) {
+  using namespace inl;
+  if (!plan) return fail(INL_E_INVALID, "attention: plan out-pointer is NULL");
+  *plan = nullptr;
+  int64_t total = 0;
+  int rc = validate_desc(desc, &total);
+  if (rc) return rc;
+  inl_attn_plan* pl = new (std::nothrow) inl_attn_plan();
+  if (!pl) return fail(INL_E_NOMEM, "attention: host allocation failed");
+  pl->desc = *desc;
+  pl->desc.cu_seqlens_host = nullptr;
+  pl->total_tokens = total;
+  rc = build_schedule(desc, &pl->sched);
+  if (rc) { delete pl; return rc; }
+  if (!pl->sched.items.empty()) {
+    const size_t bytes = pl->sched.items.size() * sizeof(int4);
+    hipError_t e = hipMalloc((void**)&pl->d_items, bytes);
+    if (e != hipSuccess) { delete pl; return hip_fail(e, "hipMalloc(plan)"); }
+    e = hipMemcpy(pl->d_items, pl->sched.items.data(), bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { (void)hipFree(pl->d_items); delete pl; return hip_fail(e, "hipMemcpy(plan)"); }
+  }
+  *plan = pl;
+  return INL_OK;
+}
+
+extern "C" int inl_attn_plan_destroy(inl_attn_plan* plan) {
+  if (!plan) return INL_OK;
+  int rc = INL_OK;
+  if (plan->d_items) {
+    hipError_t e = hipFree(plan->d_items);
+    if (e != hipSuccess) rc = inl::hip_fail(e, "hipFree(plan)");
+  }
+  delete plan;
+  return rc;
+}
+
+extern "C" int inl_attn_plan_info(const inl_attn_plan* plan, int64_t* n_tiles,
+                                  int32_t* block_m, int32_t* block_n) {
+  if (!plan) return inl::fail(INL_E_INVALID, "attention: plan is NULL");
+  if (n_tiles) *n_tiles = (int64_t)plan->sched.items.size() * (plan->desc.h_q / plan->sched.hpw);
+  if (block_m) *block_m = plan->sched.block_m;
+  if (block_n) *block_n = plan->sched.cfg.bn;
+  return INL_OK;
+}
+
+extern "C" int inl_attn_fwd(const inl_attn_plan* plan, const void* q, const void* k,
+                            const void* v, void* out, void* stream) {
+  using namespace inl;
+  if (!plan) return fail(INL_E_INVALID, "attention: plan is NULL");
+  int rc = check_ptrs(q, k, v, out, plan->total_tokens);
+  if (rc) return rc;
+  AttnParams p = make_params(&plan->desc, plan->sched, plan->d_items, q, k, v, out);
+  return launch(plan->sched.cfg, p, (int64_t)plan->sched.items.size(), (hipStream_t)stream);
+}
+
+extern "C" int inl_attn_workspace_size(const inl_attn_desc* desc, size_t* bytes) {
+  using namespace inl;
+  if (!bytes) return fail(INL_E_INVALID, "attention: bytes out-pointer is NULL");
+  int64_t total = 0;
+  int rc = validate_desc(desc, &total);
+  if (rc) return rc;
+  Schedule s;
+  rc = build_schedule(desc, &s);
+  if (rc) return rc;
+  *bytes = s.items.size() * sizeof(int4);
+  return INL_OK;
+}
+
+extern "C" int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q, const void* k,
+                                   const void* v, void* out, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  using namespace inl;
+  int64_t total = 0;
+  int rc = validate_desc(desc, &total);
+  if (rc) return rc;
+  rc = check_ptrs(q, k, v, out, total);
+  if (rc) return rc;
+  Schedule s;
+  rc = build_schedule(desc, &s);
+  if (rc) return rc;
+  const size_t need = s.items.size() * sizeof(int4);
+  if (need == 0) return INL_OK;
+  if (!workspace || workspace_bytes < need)
+    return fail(INL_E_INVALID, "attention: workspace is NULL or smaller than inl_attn_workspace_size()");
+  if (!aligned16(workspace)) return fail(INL_E_INVALID, "attention: workspace must be 16-byte aligned");
+  rc = upload_async(workspace, s.items.data(), need, (hipStream_t)stream);
+  if (rc) return rc;
+  AttnParams p = make_params(desc, s, (const int4*)workspace, q, k, v, out);
+  return launch(s.cfg, p, (int64_t)s.items.size(), (hipStream_t)stream);
+}

@@ -1,0 +1,48 @@
+// Shared definitions of the gfx950 encoder-attention library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/inl_hip.h"
+
+namespace inl {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Thread-local message of the last failure (returned by inl_last_error).
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t err, const char* what);
+
+#define INL_HIP_TRY(expr)                                   \
+  do {                                                      \
+    hipError_t inl_err_ = (expr);                           \
+    if (inl_err_ != hipSuccess) return ::inl::hip_fail(inl_err_, #expr); \
+  } while (0)
+
+inline int dtype_size(int32_t dt) { return dt == INL_BF16 ? 2 : 4; }
+inline bool dtype_ok(int32_t dt) { return dt == INL_F32 || dt == INL_BF16; }
+
+// Validate cu_seqlens (host): cu[0] == 0 and nondecreasing. Returns the token
+// count through `total`.
+int check_cu(int32_t n, const int32_t* cu, int64_t* total);
+
+// Copy a small host buffer to device memory on `stream` through the calling
+// thread's pinned staging buffer; `src` may be released when this returns.
+int upload_async(void* dst, const void* src, size_t bytes, hipStream_t stream);
+
+}  // namespace inl

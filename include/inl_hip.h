@@ -1,0 +1,222 @@
+/*
+ * inl_hip.h - C ABI of the MI355X (gfx950) encoder-attention path.
+ *
+ * The library exports plain C functions over device pointers and sizes, so
+ * that im-not-llm's Rust engines can bind it over FFI and wrap it as a candle
+ * custom op. Every pointer named `q`, `k`, `v`, `out`, `x`, `y`, `hidden`,
+ * `logits`, `pooled`, `cos`, `sin`, `weight`, `bias`, `canonical`, `rows`,
+ * `ends` is a device pointer; `cu_seqlens_host` and `lengths_host` are host
+ * pointers. Work is enqueued on `stream` (a hipStream_t; NULL = the null
+ * stream) and is asynchronous unless a function says otherwise.
+ *
+ * Errors: every function returns 0 on success and a negative INL_E_* code
+ * otherwise; inl_last_error() returns the message of the calling thread's
+ * last failure. The caller owns every buffer. Calls on one stream need no
+ * locking; calls may come from several host threads.
+ *
+ * Packed layout: texts are stored back to back, token-major. Text b owns rows
+ * [cu_seqlens[b], cu_seqlens[b+1]) of every packed tensor; a token row holds
+ * all heads contiguously (`heads * head_dim` elements), and consecutive token
+ * rows are `*_row_stride` elements apart (>= heads * head_dim), so the q, k
+ * and v slices of one fused QKV projection output can be passed without a
+ * copy. Attention never crosses texts, and RoPE positions restart at 0 for
+ * every text (the packing rule of the reference's
+ * crates/inl-ane/src/layout.rs:1-7,391-415).
+ */
+#ifndef INL_HIP_H
+#define INL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define INL_HIP_ABI_VERSION 1
+
+enum inl_status {
+  INL_OK = 0,
+  INL_E_INVALID = -1,     /* bad argument (shape, dtype, alignment, range) */
+  INL_E_UNSUPPORTED = -2, /* valid request this build has no kernel for */
+  INL_E_HIP = -3,         /* a HIP runtime call failed */
+  INL_E_NOMEM = -4        /* a host or device allocation failed */
+};
+
+enum inl_dtype { INL_F32 = 0, INL_BF16 = 1 };
+
+/* ------------------------------------------------------------------------
+ * Attention
+ *
+ * Replaces the attention call of every encoder engine:
+ *   - crates/inl-core/src/attention.rs:215-234 `attend` (Qwen3 causal GQA:
+ *     causal=1, window=-1, scale=head_dim^-0.5), with its Eager/Tiled/
+ *     CpuFlash backends (:236-315);
+ *   - crates/inl-text/src/gemma2.rs:414-441 (EmbeddingGemma 2: causal=0,
+ *     scale=1, window=sliding_window for sliding layers, -1 for full);
+ *   - crates/inl-sparse/src/modernbert.rs:366-401 (ModernBERT: causal=0,
+ *     scale=head_dim^-0.5, window=local_attention/2 on local layers);
+ *   - crates/inl-late/src/qwen3_5.rs:364-407 (Qwen3.5 full attention:
+ *     causal=is_causal, scale=head_dim^-0.5);
+ *   - crates/inl-vision/src/vision.rs:226-259 (vision tower: causal=0,
+ *     scale=1, window=-1).
+ * The reference's padded batches and additive masks become packed texts: a
+ * query i of a text sees key j of the same text iff (!causal || j <= i) and
+ * (window < 0 || |i - j| <= window). The softmax is computed in f32 for every
+ * form; QK^T products and all accumulation are f32-exact on MFMA.
+ * --------------------------------------------------------------------- */
+typedef struct inl_attn_desc {
+  int32_t n_texts;                 /* >= 0 */
+  const int32_t* cu_seqlens_host;  /* [n_texts + 1], cu[0] == 0, nondecreasing */
+  int32_t h_q;                     /* query heads */
+  int32_t h_kv;                    /* key/value heads, h_q % h_kv == 0 */
+  int32_t head_dim;                /* 8..256, multiple of 8 */
+  int32_t causal;                  /* 0 or 1 */
+  int32_t window;                  /* -1 = none, else inclusive radius >= 0 */
+  float scale;                     /* multiplies q.k before the softmax */
+  int32_t dtype;                   /* enum inl_dtype of q, k, v */
+  int32_t out_dtype;               /* enum inl_dtype of out */
+  int64_t q_row_stride;            /* elements between token rows; 0 = h_q*head_dim */
+  int64_t k_row_stride;            /* 0 = h_kv*head_dim */
+  int64_t v_row_stride;            /* 0 = h_kv*head_dim */
+  int64_t o_row_stride;            /* 0 = h_q*head_dim */
+  int32_t flags;                   /* INL_ATTN_* bits, 0 = defaults */
+} inl_attn_desc;
+
+/* bf16 inputs: the PV product runs in fp16 by default (V converted exactly
+ * while staged, P rounded to fp16: |v| must stay below 65504, larger values
+ * become inf). This flag keeps V and P in bf16 (any range, 8x coarser P). */
+#define INL_ATTN_PV_BF16 1
+
+/* An attention plan: the packed texts' tile schedule, resident on the
+ * device. Build it once per batch and reuse it for every layer of that
+ * batch that has the same desc fields (all layers of one kind). */
+typedef struct inl_attn_plan inl_attn_plan;
+
+/* Build a plan (host work + one blocking upload). The desc's pointer fields
+ * are read during the call only. */
+int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** plan);
+int inl_attn_plan_destroy(inl_attn_plan* plan);
+/* Tiles the plan launches and query rows each covers (for reporting). */
+int inl_attn_plan_info(const inl_attn_plan* plan, int64_t* n_tiles,
+                       int32_t* block_m, int32_t* block_n);
+
+/* out[N, h_q, head_dim] = attention(q[N, h_q, d], k[N, h_kv, d], v[N, h_kv, d]). */
+int inl_attn_fwd(const inl_attn_plan* plan, const void* q, const void* k,
+                 const void* v, void* out, void* stream);
+
+/* One-shot form: plans into `workspace` (device memory of at least
+ * inl_attn_workspace_size() bytes) and launches. */
+int inl_attn_workspace_size(const inl_attn_desc* desc, size_t* bytes);
+int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q,
+                        const void* k, const void* v, void* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Prologue: fused per-head RMSNorm + RoPE over packed rows.
+ *
+ * Replaces q_norm/k_norm + rope of crates/inl-text/src/qwen3/mod.rs:236-249
+ * (RmsNorm :72-90, RotaryTable :123-159), the q/k/v norms and rope of
+ * gemma2.rs:389-410, rope_thd of modernbert.rs:264-269, the zero-centred
+ * norms (weight = 1 + w, folded by the caller) and partial RoPE of
+ * qwen3_5.rs:188-206,289-300, and the axial RoPE of vision.rs:792-800.
+ *
+ * y = rope(rms_norm(x) * weight) per (token, head) row of head_dim elements:
+ *   norm:  x / sqrt(mean(x^2) + eps) * weight   (weight NULL = all ones;
+ *          norm == 0 skips the norm);
+ *   rope:  sections == 1: the first rotary_dim features are rotated in
+ *          half-split pairs (i, i + rotary_dim/2) with cos/sin row `pos`,
+ *          where pos = the row's position inside its text; the rest pass
+ *          through. sections == 2 (axial): each half of the head is rotated
+ *          by its own half-split with tables cos/sin (first half) and
+ *          cos2/sin2 (second half), indexed by the packed token row.
+ *          rotary_dim == 0 skips the rope.
+ * Tables are f32 `[rows, table_width]`; with round_tables=1 every table value
+ * is rounded to bf16 first (the reference stores them in the model dtype).
+ * With round_norm=1 the normalised value is rounded to the output dtype
+ * before the rotation (the reference materialises it in the model dtype).
+ * --------------------------------------------------------------------- */
+typedef struct inl_norm_rope_desc {
+  int32_t n_texts;
+  const int32_t* cu_seqlens_host; /* [n_texts + 1] */
+  int32_t heads;
+  int32_t head_dim;               /* even, <= 512 */
+  int64_t x_row_stride;           /* 0 = heads*head_dim */
+  int64_t y_row_stride;           /* 0 = heads*head_dim */
+  int32_t dtype;                  /* x dtype */
+  int32_t out_dtype;              /* y dtype */
+  int32_t norm;                   /* 1 = apply the RMSNorm */
+  float eps;
+  int32_t rotary_dim;             /* 0 = no rope; sections==1: even <= head_dim */
+  int32_t sections;               /* 1 = half-split, 2 = axial */
+  int32_t table_rows;             /* rows in cos/sin (positions or tokens) */
+  int32_t round_tables;
+  int32_t round_norm;
+} inl_norm_rope_desc;
+
+int inl_norm_rope_fwd(const inl_norm_rope_desc* desc, const void* x,
+                      void* y, const void* weight /* [head_dim] dtype or NULL */,
+                      const float* cos, const float* sin,
+                      const float* cos2, const float* sin2, void* stream);
+
+/* Host helper: RoPE tables as the reference builds them.
+ * mode 0: inv_freq and angles in f64, stored f32 (qwen3/mod.rs:131-153,
+ *         gemma2.rs:292-315, modernbert.rs:239-262);
+ * mode 1: in f32 (qwen3_5.rs:940-957). cos/sin are host [positions, dim/2]. */
+int inl_rope_table_host(int32_t rotary_dim, double theta, int32_t positions,
+                        int32_t mode, float* cos_out, float* sin_out);
+
+/* ------------------------------------------------------------------------
+ * Epilogues
+ * --------------------------------------------------------------------- */
+
+/* Last-token pooling: pooled[b] = l2(rms_norm(hidden[cu[b+1]-1]) * weight),
+ * f32 output [n_texts, hidden_dim]. Replaces qwen3/mod.rs:356-357 + :464-469.
+ * round_norm=1 rounds the normed row to `dtype` before the L2 (the reference
+ * keeps it in the model dtype). Empty texts yield zero rows. */
+int inl_pool_last_fwd(int32_t n_texts, const int32_t* cu_seqlens_host,
+                      int32_t hidden_dim, int64_t row_stride, int32_t dtype,
+                      const void* hidden, const void* weight, float eps,
+                      int32_t round_norm, float* pooled, void* stream);
+
+/* Mean pooling: pooled[b] = sum_{rows of b} hidden / len_b, f32 output
+ * [n_texts, hidden_dim] (gemma2.rs:647-656). normalize=1 also L2-normalises
+ * (gemma2.rs:660-661, when the projection is the identity). */
+int inl_pool_mean_fwd(int32_t n_texts, const int32_t* cu_seqlens_host,
+                      int32_t hidden_dim, int64_t row_stride, int32_t dtype,
+                      const void* hidden, int32_t normalize, float* pooled,
+                      void* stream);
+
+/* Row-wise L2 normalisation of the first `dim` entries of f32 rows (in
+ * place allowed): x / sqrt(sum x^2 + eps_inside). eps_inside = 1e-12 is the
+ * pooled-embedding norm (qwen3/mod.rs:468); eps_inside = 0 with
+ * skip_zero = 1 is Matryoshka truncate-and-renormalise
+ * (crates/inl-text/src/native.rs:822-830). */
+int inl_l2_normalize_fwd(int32_t rows, int32_t dim, int64_t in_stride,
+                         const float* x, int64_t out_stride, float* y,
+                         float eps_inside, int32_t skip_zero, void* stream);
+
+/* SPLADE pooling (crates/inl-sparse/src/modernbert.rs:806-907):
+ *   m[r, t]  = max over speaking positions p in [ends[r-1], ends[r]) of
+ *              logits[p, t]   (f32 [n_speak, vocab], bias-free);
+ *   w[r, t]  = ln(relu(m + bias[t] - shift) * open[t] + 1), open[t] = 0 for
+ *              t in masked_ids, -inf max (no speaker) gives 0;
+ *   out[r,c] = max(0, max over t with canonical[t] == c of w[r, t])
+ *              (canonical NULL: out = w, out_dim == vocab).
+ * ends_host: [rows] host, exclusive ends. out: f32 [rows, out_dim]. */
+int inl_pool_splade_fwd(int32_t rows, const int64_t* ends_host, int32_t vocab,
+                        const float* logits, int64_t logits_stride,
+                        const float* bias, float shift,
+                        const int32_t* masked_ids_host, int32_t n_masked,
+                        const int32_t* canonical, int32_t out_dim, float* out,
+                        void* stream);
+
+/* ------------------------------------------------------------------------ */
+const char* inl_last_error(void);
+int32_t inl_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INL_HIP_H */

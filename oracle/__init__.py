@@ -1,0 +1,25 @@
+"""CPU oracle for the encoder attention path. TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU and in plain numpy (float64 unless a
+function says otherwise), the arithmetic the reference im-not-llm candle
+implementation performs on the encoder attention hot path:
+
+* ``attention``  - the five attention forms (Qwen3 causal GQA, EmbeddingGemma
+  bidirectional full/sliding, ModernBERT global/local, Qwen3.5 full attention,
+  vision ViT) over padded batches with the reference's additive masks, and the
+  packed variable-length form the HIP kernels implement;
+* ``prologue``   - per-head RMSNorm and the half-split / partial / axial RoPE;
+* ``pooling``    - last-token, mean and SPLADE epilogues, L2 normalisation,
+  Matryoshka truncation and the sparse active-term set;
+* ``tiny_models`` - the tiny EmbeddingGemma 2 and ModernBERT-SPLADE encoders
+  of the reference's golden fixtures, used to pin the forms above in situ;
+* ``cref``       - a ctypes loader for ``attn_ref.c``, the multi-threaded f32
+  C restatement used as the CPU baseline.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this package, and only as the checker: the
+product path (``im-not-llm_amd/``) never calls into it.
+
+Every function cites the reference file:line it follows (paths relative to
+the reference repository root).
+"""

@@ -1,0 +1,159 @@
+"""GPU parity: the HIP varlen attention against the numpy oracle.
+
+Inputs are seeded; bf16 cases compare against the float64 oracle evaluated on
+the same bf16-rounded inputs. Tolerances (north star): attention output
+max-abs error <= 2e-3 in bf16 (checked on f32 output, so the bound covers
+the kernel's arithmetic: bf16 MFMA products, bf16 P, fp32 softmax and
+accumulation) plus, for bf16 output, the output's own rounding
+(half a bf16 ulp of the value); <= 1e-5 in f32 mode.
+"""
+import numpy as np
+import pytest
+
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(lengths, hq, hkv, d, seed, dtype, torch, dev, scale=None, logit_std=1.0):
+    """N(0,1) q/k/v; q and k RMS-normalised per head (as the prologue leaves
+    them), q then scaled so that ``scale * q.k`` has std ``logit_std``."""
+    rng = np.random.default_rng(seed)
+    n = int(sum(lengths))
+    q = rng.standard_normal((n, hq, d)).astype(np.float32)
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    q /= np.sqrt((q * q).mean(-1, keepdims=True) + 1e-6)
+    k /= np.sqrt((k * k).mean(-1, keepdims=True) + 1e-6)
+    if scale is not None:
+        q *= np.float32(logit_std * d ** -0.5 / scale)
+    ts = [torch.from_numpy(x).to(dev).to(dtype) for x in (q, k, v)]
+    host = [t.float().cpu().numpy().astype(np.float64) for t in ts]
+    return ts, host
+
+
+def _half_ulp_bf16(x):
+    # half a bf16 ulp of |x|: 2^(floor(log2|x|) - 8)
+    ax = np.maximum(np.abs(x), 1e-30)
+    return np.exp2(np.floor(np.log2(ax)) - 8)
+
+
+CASES = [
+    # (name, lengths, hq, hkv, d, causal, window, scale)
+    ("qwen3_causal_gqa", [1, 2, 31, 32, 33, 64, 65, 127, 200, 300], 16, 8, 128, True, -1, 128 ** -0.5),
+    ("gemma_full_gqa3", [5, 70, 129, 257], 3, 1, 256, False, -1, 1.0),
+    ("gemma_sliding", [3, 100, 700, 1100], 3, 1, 256, False, 512, 1.0),
+    ("modernbert_local", [1, 40, 129, 300], 12, 12, 64, False, 64, 64 ** -0.5),
+    ("modernbert_global", [2, 97, 260], 12, 12, 64, False, -1, 64 ** -0.5),
+    ("vision_full", [256, 256, 17], 16, 16, 64, False, -1, 1.0),
+    ("qwen35_causal_d256", [1, 77, 300], 16, 2, 256, True, -1, 256 ** -0.5),
+    ("causal_window", [90, 200], 4, 2, 128, True, 16, 128 ** -0.5),
+    ("tiny_head_dims", [9, 13], 4, 2, 16, False, 3, 1.0),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_bf16_matches_oracle(case, cuda, inl):
+    import torch
+    name, lengths, hq, hkv, d, causal, window, scale = case
+    (q, k, v), (qh, kh, vh) = _inputs(lengths, hq, hkv, d, 1, torch.bfloat16, torch, cuda, scale)
+    cu = oa.cu_from_lengths(lengths)
+    ref = oa.varlen_attention(qh, kh, vh, cu, causal=causal, window=window, scale=scale)
+    print(f"case={name} lengths={lengths}", flush=True)
+    out32 = inl.varlen_attention(q, k, v, cu.tolist(), causal=causal, window=window,
+                                 scale=scale, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    err = np.abs(out32.cpu().numpy().astype(np.float64) - ref)
+    assert err.max() <= 2e-3, f"{name}: max abs err {err.max():.3g} (f32 out)"
+    out16 = inl.varlen_attention(q, k, v, cu.tolist(), causal=causal, window=window, scale=scale)
+    torch.cuda.synchronize()
+    got = out16.float().cpu().numpy().astype(np.float64)
+    bound = 2e-3 + _half_ulp_bf16(ref)
+    assert np.all(np.abs(got - ref) <= bound), f"{name}: bf16 out beyond 2e-3 + half ulp"
+
+
+F32_CASES = [c for c in CASES if c[0] in (
+    "qwen3_causal_gqa", "gemma_sliding", "modernbert_local", "tiny_head_dims", "qwen35_causal_d256")]
+
+
+@pytest.mark.parametrize("case", F32_CASES, ids=[c[0] for c in F32_CASES])
+def test_f32_matches_oracle(case, cuda, inl):
+    import torch
+    name, lengths, hq, hkv, d, causal, window, scale = case
+    (q, k, v), (qh, kh, vh) = _inputs(lengths, hq, hkv, d, 2, torch.float32, torch, cuda, scale)
+    cu = oa.cu_from_lengths(lengths)
+    ref = oa.varlen_attention(qh, kh, vh, cu, causal=causal, window=window, scale=scale)
+    print(f"case={name} f32", flush=True)
+    out = inl.varlen_attention(q, k, v, cu.tolist(), causal=causal, window=window, scale=scale)
+    torch.cuda.synchronize()
+    err = np.abs(out.cpu().numpy().astype(np.float64) - ref).max()
+    assert err <= 1e-5, f"{name}: f32 max abs err {err:.3g}"
+
+
+def test_plan_reuse_and_empty_texts(cuda, inl):
+    """A plan is reusable across calls; zero-length texts own no rows."""
+    import torch
+    lengths = [0, 50, 0, 1, 130, 0]
+    (q, k, v), (qh, kh, vh) = _inputs(lengths, 8, 4, 128, 3, torch.bfloat16, torch, cuda)
+    cu = oa.cu_from_lengths(lengths)
+    desc = inl.make_attn_desc(cu.tolist(), 8, 4, 128, causal=True, dtype="bf16", out_dtype="f32")
+    plan = inl.AttnPlan(desc)
+    ref = oa.varlen_attention(qh, kh, vh, cu, causal=True, scale=128 ** -0.5)
+    for _ in range(3):
+        out = torch.full((q.shape[0], 8, 128), float("nan"), device=cuda)
+        plan.run(q, k, v, out)
+        torch.cuda.synchronize()
+        assert np.abs(out.cpu().numpy() - ref).max() <= 2e-3
+    plan.close()
+
+
+def test_fused_qkv_strided_rows(cuda, inl):
+    """q, k, v as column slices of one fused projection output."""
+    import torch
+    lengths = [33, 100]
+    n, hq, hkv, d = sum(lengths), 16, 8, 128
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(n, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16).to(cuda)
+    q = qkv[:, : hq * d].view(n, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(n, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(n, hkv, d)
+    cu = oa.cu_from_lengths(lengths)
+    ref = oa.varlen_attention(*(t.float().cpu().numpy().astype(np.float64) for t in (q, k, v)),
+                              cu, causal=True, scale=d ** -0.5)
+    out = inl.varlen_attention(q, k, v, cu.tolist(), causal=True, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert np.abs(out.cpu().numpy() - ref).max() <= 2e-3
+
+
+def test_config2_batch_bf16(cuda, inl):
+    """The first 64-text batch of the config-2 workload (log-normal lengths,
+    median 180, max 2048), causal GQA 16/8 x 128, q/k RMS-normalised N(0,1)."""
+    import torch
+    from inl_hip import workloads
+    lengths = workloads.batches(workloads.qwen3_op_lengths())[0]
+    (q, k, v), (qh, kh, vh) = _inputs(lengths, 16, 8, 128, 0, torch.bfloat16, torch, cuda)
+    cu = oa.cu_from_lengths(lengths)
+    ref = oa.varlen_attention(qh, kh, vh, cu, causal=True, scale=128 ** -0.5)
+    out = inl.varlen_attention(q, k, v, cu.tolist(), causal=True, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    err = np.abs(out.cpu().numpy() - ref).max()
+    print(f"config2 batch0 tokens={sum(lengths)} max abs err={err:.3g}", flush=True)
+    assert err <= 2e-3
+
+
+@pytest.mark.parametrize("pv_bf16", [False, True], ids=["pv_f16", "pv_bf16"])
+def test_peaky_logits_bf16(pv_bf16, cuda, inl):
+    """Logit std 4 (few keys carry the weight) stresses the rounding of P:
+    fp16 P stays within 2e-3; the bf16-P option is bounded by 8e-3."""
+    import torch
+    lengths = [2, 3, 5, 17, 130]
+    (q, k, v), (qh, kh, vh) = _inputs(lengths, 8, 4, 128, 7, torch.bfloat16, torch, cuda,
+                                      128 ** -0.5, logit_std=4.0)
+    cu = oa.cu_from_lengths(lengths)
+    ref = oa.varlen_attention(qh, kh, vh, cu, causal=True, scale=128 ** -0.5)
+    out = inl.varlen_attention(q, k, v, cu.tolist(), causal=True, out_dtype=torch.float32,
+                               flags=inl.ATTN_PV_BF16 if pv_bf16 else 0)
+    torch.cuda.synchronize()
+    err = np.abs(out.cpu().numpy() - ref).max()
+    print(f"peaky pv_bf16={pv_bf16} max abs err={err:.3g}", flush=True)
+    assert err <= (8e-3 if pv_bf16 else 2e-3)
