@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""Benchmark of the encoder attention hot path on one MI355X.
+
+Default workload (the metric's configuration):
+packed variable-length causal GQA attention at the Qwen3-0.6B shape
+(16 query heads, 8 KV heads, head_dim 128, bf16), 713 texts with log-normal
+lengths (median 180, sigma 1.0, max 2048; 200,179 tokens) in 12 batches of
+64 texts. Q/K/V are N(0,1) after a seeded RMSNorm. A step is one pass of
+the attention op over all 12 batches (12 launches, one plan per batch built
+before timing, as an engine builds one per batch and reuses it for every
+layer).
+
+Prints one JSON line: tokens/s (value), attention TFLOP/s, the roofline of
+the attention kernel (algorithmic FLOPs / kernel time from HIP events on the
+launch stream, against the 2516.6 TFLOP/s bf16 dense MFMA peak) and the CPU
+baseline (the oracle's multi-threaded f32 C restatement of the reference
+CPU flash path, timed on a bounded sample of the same workload).
+
+Other workloads (--workload): gemma_window, gemma_full, modernbert_local,
+modernbert_global, vision, pplx_causal - reported the same way.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "im-not-llm_amd"))
+
+METRIC = "encoded tokens/sec + attention TFLOP/s (% bf16 MFMA peak), Qwen3-0.6B-shape"
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 flop/clk/CU, dense
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def workload(name: str):
+    """(lengths per batch, h_q, h_kv, head_dim, causal, window, scale, label)."""
+    from inl_hip import workloads as w
+    if name == "qwen3":
+        lens = w.qwen3_op_lengths()
+        return (w.batches(lens, 64), 16, 8, 128, True, -1, 128 ** -0.5,
+                "config2: packed causal GQA attention, Qwen3-0.6B shape (16 Q / 8 KV heads, "
+                "head_dim 128, bf16); 713 texts log-normal(median 180, sigma 1.0, max 2048) = "
+                f"{sum(lens)} tokens in 12 batches of 64")
+    if name in ("gemma_window", "gemma_full"):
+        lens = w.uniform_lengths(32, 64, 8192)
+        win = 512 if name == "gemma_window" else -1
+        return ([lens], 3, 1, 256, False, win, 1.0,
+                f"config3: EmbeddingGemma-text bidirectional attention, 3 Q / 1 KV heads, head_dim "
+                f"256, {'sliding radius 512' if win > 0 else 'full'}; 32 texts U[64,8192] = {sum(lens)} tokens")
+    if name in ("modernbert_local", "modernbert_global"):
+        lens = w.uniform_lengths(128, 32, 2048)
+        win = 64 if name == "modernbert_local" else -1
+        return ([lens], 12, 12, 64, False, win, 64 ** -0.5,
+                f"config4: ModernBERT attention, 12 heads x 64, {'local radius 64' if win > 0 else 'global'}; "
+                f"128 texts U[32,2048] = {sum(lens)} tokens")
+    if name == "pplx_causal":
+        lens = [4096] * 16
+        return ([lens], 16, 2, 256, True, -1, 256 ** -0.5,
+                "config5a: pplx-late full attention, causal GQA 16 Q / 2 KV heads x 256; 16 texts x 4096")
+    if name == "vision":
+        lens = [256] * 64
+        return ([lens], 16, 16, 64, False, -1, 1.0,
+                "config5b: vision ViT block attention, 16 heads x 64, bidirectional; 64 images x 256 patches")
+    raise SystemExit(f"unknown workload {name}")
+
+
+def make_inputs(lengths, hq, hkv, d, scale, seed, torch, dev):
+    """Seeded N(0,1) q/k/v through an RMSNorm with weights 1 + 0.2 u (u in
+    [-0.5, 0.5)), q scaled so that scale * q.k has unit variance; bf16."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    n = int(sum(lengths))
+
+    def normed(h, s):
+        x = torch.randn(n, h, d, generator=g, device=dev)
+        w = 1.0 + 0.2 * (torch.rand(d, generator=g, device=dev) - 0.5)
+        x = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6) * w
+        return (x * s).to(torch.bfloat16)
+
+    q = normed(hq, d ** -0.5 / scale)
+    k = normed(hkv, 1.0)
+    v = normed(hkv, 1.0)
+    return q, k, v
+
+
+def cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale, seconds):
+    """The oracle's f32 C restatement on host cores over consecutive batches
+    of the same workload until `seconds` of work (at least one batch)."""
+    from oracle import cref, attention as oa
+    cref.lib()
+    tokens, flops, spent, used = 0, 0, 0.0, 0
+    for lens, (q, k, v) in zip(batches, inputs):
+        qh, kh, vh = (t.float().cpu().numpy() for t in (q, k, v))
+        cu = oa.cu_from_lengths(lens)
+        t0 = time.perf_counter()
+        cref.attention_f32(qh, kh, vh, cu, causal=causal, window=window, scale=scale)
+        spent += time.perf_counter() - t0
+        tokens += int(sum(lens))
+        flops += oa.attention_flops(lens, hq, d, causal, window)
+        used += 1
+        if spent >= seconds:
+            break
+    return {
+        "value": round(tokens / spent, 1),
+        "unit": "tokens/s",
+        "cores": cref.threads(),
+        "kind": "port",
+        "sample": (f"first {used} of {len(batches)} batches ({tokens} tokens, "
+                   f"{flops / 1e12:.4f} TFLOP) through oracle/attn_ref.c (f32 per-text online-softmax "
+                   f"attention, OpenMP), {spent:.2f} s"),
+        "tflops": round(flops / spent / 1e12, 4),
+    }
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch from the committed PMC summary, if present."""
+    f = ROOT / "profiles" / f"attn_fwd_{name}_pmc.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="qwen3")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the path shards by independent texts, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import inl_hip
+    from inl_hip import attention_flops
+
+    dev = torch.device("cuda:0")
+    batches, hq, hkv, d, causal, window, scale, label = workload(args.workload)
+    inputs = [make_inputs(lens, hq, hkv, d, scale, 1000 + i, torch, dev) for i, lens in enumerate(batches)]
+    plans, outs = [], []
+    for lens, (q, k, v) in zip(batches, inputs):
+        cu = inl_hip.workloads.cu_seqlens(lens)
+        desc = inl_hip.make_attn_desc(cu, hq, hkv, d, causal=causal, window=window, scale=scale,
+                                      dtype="bf16", out_dtype="bf16")
+        plans.append(inl_hip.AttnPlan(desc))
+        outs.append(torch.empty_like(q))
+    tokens = sum(sum(b) for b in batches)
+    flops = sum(attention_flops(b, hq, d, causal, window) for b in batches)
+    n_launch = len(batches)
+    stream = torch.cuda.current_stream()
+    log(f"workload: {label}; {flops / 1e12:.4f} TFLOP per step, {n_launch} launches")
+
+    def step(evs=None):
+        for i, (pl, (q, k, v), o) in enumerate(zip(plans, inputs, outs)):
+            if evs is not None:
+                evs[i][0].record(stream)
+            pl.run(q, k, v, o, stream)
+            if evs is not None:
+                evs[i][1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    events = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+               for _ in range(n_launch)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(events[s])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    kernel_ms = sum(a.elapsed_time(b) for ev in events for a, b in ev)
+    avg_launch_ms = kernel_ms / (args.steps * n_launch)
+    achieved = flops / n_launch / (avg_launch_ms * 1e-3) / 1e12
+    tok_s = tokens * args.steps / wall
+    traffic = read_traffic(args.workload)
+    log(f"wall {wall:.4f} s for {args.steps} steps; kernel {kernel_ms:.3f} ms; "
+        f"avg launch {avg_launch_ms * 1e3:.1f} us; {achieved:.1f} TFLOP/s")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v after RMSNorm; no checkpoint)",
+        "config": {"workload": label, "tokens_per_step": tokens, "launches_per_step": n_launch,
+                   "attention_tflop_per_step": round(flops / 1e12, 6)},
+        "attention_tflops": round(flops * args.steps / wall / 1e12, 2),
+        "attention_frac_of_peak": round(flops * args.steps / wall / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel": "attn_fwd_kernel<bf16, D=128, BN=64, NW=4, PV16>",
+            "avg_launch_us": round(avg_launch_ms * 1e3, 2),
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale,
+                                              args.cpu_seconds)
+    for pl in plans:
+        pl.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -44,49 +44,17 @@
 #include <new>
 #include <vector>
 
-#include "inl_common.hpp"
+#include "attn_kernels.hpp"
 
 namespace inl {
 
 namespace {
-
-struct AttnParams {
-  const char* q;
-  const char* k;
-  const char* v;
-  char* o;
-  int64_t q_stride, k_stride, v_stride, o_stride;  // elements between token rows
-  const int4* items;  // {seg_start, seg_len, q0, (lo_tile << 16) | hi_tile}
-  int32_t n_hg;       // workgroups per item
-  int32_t groups_per_kv;  // (h_q / h_kv) / hpw
-  int32_t group;      // h_q / h_kv
-  int32_t hpw;        // query heads per workgroup
-  int32_t rb;         // 32-row blocks per head per workgroup (NW / hpw)
-  int32_t head_dim;
-  int32_t causal;
-  int32_t window;
-  float scale_log2;   // scale * log2(e)
-  int32_t out_bf16;
-};
 
 // Element type of V^T in LDS and of P for the PV product.
 template <typename E, bool PV16>
 struct PvType { typedef float T; };
 template <> struct PvType<bf16, true> { typedef f16 T; };
 template <> struct PvType<bf16, false> { typedef bf16 T; };
-
-constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ float wave_xor32(float x) {
-  return __shfl_xor(x, 32, 64);
-}
-
-// Byte offset of 16-byte chunk `c` of row `r` in a row-major tile whose rows
-// are `row_bytes` long. The XOR keeps the 8 rows a group of lanes reads at
-// one logical chunk in 8 distinct chunk columns (bank-conflict free).
-__device__ __forceinline__ int swz(int r, int c, int row_bytes) {
-  return r * row_bytes + ((c ^ (r & 7)) << 4);
-}
 
 // Column of a 4-key group inside a V^T row. bf16: within 16 keys, swap key
 // bits 2 and 3, so lane-half h of the PV product reads its 8 keys
@@ -460,8 +428,18 @@ KernelCfg make_cfg() {
   return KernelCfg{attn_fwd_kernel<E, D, BN, NW, PV16>, D, BN, NW, 4 * BN * D * (int)sizeof(E)};
 }
 
-int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, KernelCfg* cfg) {
+// `fits32`: every text's q/k/v rows span < 4 GiB, as the fast kernel's
+// 32-bit buffer offsets need.
+int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, bool fits32, KernelCfg* cfg) {
   const bool pv16 = !(flags & INL_ATTN_PV_BF16);
+  if (dtype == INL_BF16 && pv16 && fits32) {
+    AttnKernelFn fn;
+    int bn, nw, lds;
+    if (bf16_fast_kernel(head_dim, &fn, &bn, &nw, &lds)) {
+      *cfg = KernelCfg{fn, head_dim, bn, nw, lds};
+      return INL_OK;
+    }
+  }
   if (dtype == INL_BF16) {
     if (head_dim <= 64) *cfg = pv16 ? make_cfg<bf16, 64, 64, 4, true>() : make_cfg<bf16, 64, 64, 4, false>();
     else if (head_dim <= 128) *cfg = pv16 ? make_cfg<bf16, 128, 64, 4, true>() : make_cfg<bf16, 128, 64, 4, false>();
@@ -531,7 +509,16 @@ struct Schedule {
 };
 
 int build_schedule(const inl_attn_desc* d, Schedule* s) {
-  int rc = select_kernel(d->dtype, d->head_dim, d->flags, &s->cfg);
+  int64_t max_t = 0;
+  for (int b = 0; b < d->n_texts; ++b)
+    max_t = std::max<int64_t>(max_t, d->cu_seqlens_host[b + 1] - d->cu_seqlens_host[b]);
+  const int es = dtype_size(d->dtype);
+  const int64_t qs = d->q_row_stride ? d->q_row_stride : (int64_t)d->h_q * d->head_dim;
+  const int64_t ks = d->k_row_stride ? d->k_row_stride : (int64_t)d->h_kv * d->head_dim;
+  const int64_t vs = d->v_row_stride ? d->v_row_stride : (int64_t)d->h_kv * d->head_dim;
+  const int64_t widest = std::max(qs, std::max(ks, vs)) * es;
+  const bool fits32 = (max_t + 256) * widest < ((int64_t)1 << 32);
+  int rc = select_kernel(d->dtype, d->head_dim, d->flags, fits32, &s->cfg);
   if (rc) return rc;
   const int group = d->h_q / d->h_kv;
   s->hpw = heads_per_wg(group, s->cfg.nw);

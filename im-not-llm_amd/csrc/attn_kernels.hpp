@@ -1,0 +1,45 @@
+// Kernel-side definitions shared by the attention kernels.
+#pragma once
+
+#include "inl_common.hpp"
+
+namespace inl {
+
+struct AttnParams {
+  const char* q;
+  const char* k;
+  const char* v;
+  char* o;
+  int64_t q_stride, k_stride, v_stride, o_stride;  // elements between token rows
+  const int4* items;  // {seg_start, seg_len, q0, (lo_tile << 16) | hi_tile}
+  int32_t n_hg;       // workgroups per item
+  int32_t groups_per_kv;  // (h_q / h_kv) / hpw
+  int32_t group;      // h_q / h_kv
+  int32_t hpw;        // query heads per workgroup
+  int32_t rb;         // 32-row blocks per head per workgroup (NW / hpw)
+  int32_t head_dim;
+  int32_t causal;
+  int32_t window;
+  float scale_log2;   // scale * log2(e)
+  int32_t out_bf16;
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float wave_xor32(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+// Byte offset of 16-byte chunk `c` of row `r` in a row-major tile whose rows
+// are `row_bytes` long. The XOR keeps the 8 rows a group of lanes reads at
+// one logical chunk in 8 distinct chunk columns (bank-conflict free).
+__device__ __forceinline__ int swz(int r, int c, int row_bytes) {
+  return r * row_bytes + ((c ^ (r & 7)) << 4);
+}
+
+// Launch of the bf16 fast path (attn_fwd_bf16.hip): returns the kernel entry
+// and its dynamic LDS size for head dims 64/128/256.
+typedef void (*AttnKernelFn)(AttnParams);
+bool bf16_fast_kernel(int head_dim_padded, AttnKernelFn* fn, int* bn, int* nw, int* lds);
+
+}  // namespace inl
