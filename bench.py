@@ -61,6 +61,12 @@ def workload(name: str):
         return ([lens], 12, 12, 64, False, win, 64 ** -0.5,
                 f"config4: ModernBERT attention, 12 heads x 64, {'local radius 64' if win > 0 else 'global'}; "
                 f"128 texts U[32,2048] = {sum(lens)} tokens")
+    if name in ("qwen3_2048", "qwen3_2048_full"):
+        lens = [2048] * 32
+        causal = name == "qwen3_2048"
+        return ([lens], 16, 8, 128, causal, -1, 128 ** -0.5,
+                f"Qwen3-0.6B-shape attention at 2048-token texts ({'causal' if causal else 'bidirectional'} "
+                "GQA 16 Q / 8 KV heads x 128, bf16); 32 texts x 2048")
     if name == "pplx_causal":
         lens = [4096] * 16
         return ([lens], 16, 2, 256, True, -1, 256 ** -0.5,

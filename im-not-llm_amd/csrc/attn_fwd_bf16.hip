@@ -8,7 +8,8 @@
 //     which writes the XOR-swizzled layout the ds_read_b128 of the S^T
 //     product reads without bank conflicts.
 //   - V tiles are loaded to registers (buffer loads), converted bf16 -> fp16
-//     and stored row-major; the PV product reads them transposed with
+//     and stored row-major (rows padded by 32 bytes); the PV product reads
+//     them transposed with
 //     `ds_read_b64_tr_b16` (within 16 lanes, lane j receives element j % 4 of
 //     the 8 bytes addressed by lanes 4e + j / 4, e = 0..3), so no transpose
 //     is done by ALU instructions.
@@ -16,6 +17,8 @@
 //     zero, so no load needs a branch.
 // The kernel requires head_dim == D (64, 128 or 256); other head dims take
 // the generic kernel.
+
+#include <type_traits>
 
 #include "attn_kernels.hpp"
 
@@ -33,23 +36,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Byte offset in a V (fp16, row-major, D columns) tile: 16-byte chunk c of
-// row r is XOR-ed with 2 * (r & 3), so the four rows one 16-lane group of a
-// transposed read touches fall on four distinct 32-byte bank ranges.
+// V tiles are stored fp16, row-major, with rows padded by 32 bytes: a 16-lane
+// transposed read touches 4 consecutive rows x 2 chunks, and a row pitch of
+// 2 (mod 8) 16-byte units puts those 8 chunks in 8 distinct bank groups while
+// every fragment offset stays linear in (ks, db).
 template <int D>
-__device__ __forceinline__ int vswz(int r, int c) {
-  return r * (D * 2) + ((c ^ ((r & 3) << 1)) << 4);
-}
+constexpr int vrow_bytes() { return D * 2 + 32; }
 
-// D = 256 keeps 128 KB of LDS per workgroup (one per CU), so it is built
-// for one wave per SIMD and the whole register file.
+// max / sum of a value over the two lanes l and l ^ 32 (v_permlane32_swap).
+__device__ __forceinline__ float wave_max_halves(float x) { return fmaxf(x, wave_xor32(x)); }
+__device__ __forceinline__ float wave_sum_halves(float x) { return x + wave_xor32(x); }
+
+// D = 256 needs ~300 registers (O^T alone is 128) and 136 KB of LDS, one
+// workgroup per CU: it is built for one wave per SIMD.
 template <int D, int BN, int NW>
 __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(AttnParams p) {
   constexpr int NT = NW * 64;
   constexpr int CH = D / 8;               // 16-byte chunks per row
   constexpr int ROW = D * 2;              // bytes per K or V row in LDS
-  constexpr int TILE = BN * ROW;          // bytes of one K (or V) tile
-  constexpr int STAGE = 2 * TILE;         // K tile + V tile
+  constexpr int TILE = BN * ROW;          // bytes of one K tile
+  constexpr int VROWB = vrow_bytes<D>();  // bytes per V row in LDS (padded)
+  constexpr int STAGE = TILE + BN * VROWB;  // K tile + V tile
   constexpr int KBLK = TILE / 1024;       // 1 KB direct-load blocks per K tile
   constexpr int KPT = KBLK / NW;          // direct loads per wave per tile
   constexpr int VPT = (BN * CH) / NT;     // V chunks per thread per tile
@@ -62,7 +69,7 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lq = lane & 31;
   const int hf = lane >> 5;
 
@@ -145,7 +152,7 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
         f32x2 x = {__builtin_bit_cast(float, w[j] << 16), __builtin_bit_cast(float, w[j] & 0xffff0000u)};
         o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2));
       }
-      *reinterpret_cast<u32x4*>(sV + vswz<D>(row, c)) = o;
+      *reinterpret_cast<u32x4*>(sV + row * VROWB + c * 16) = o;
     }
   };
 
@@ -160,33 +167,54 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
   const int g16 = lane >> 4;        // 16-lane group of the transposed reads
   const int j16 = lane & 15;
 
+  // Per-lane LDS byte offsets that do not change across tiles.
+  int koff[D / 16];                 // K fragment of step st, row lq (+ kb*32 rows)
+#pragma unroll
+  for (int st = 0; st < D / 16; ++st) koff[st] = lq * ROW + (((2 * st + hf) ^ (lq & 7)) << 4);
+  const int vcol = 16 * (g16 & 1) + 4 * (j16 & 3);
+  const int vrow = 4 * hf + (j16 >> 2);
+  // V^T fragment (db, ks, half): rows ks*16 + 8*half + vrow, columns
+  // db*32 + vcol, at a linear offset from this per-lane base.
+  const int vbase_off = vrow * VROWB + vcol * 2;
+
   for (int t = lo_t; t < hi_t; ++t) {
     const int buf = (t - lo_t) & 1;
     const bool more = t + 1 < hi_t;
     if (more) issue(t + 1, buf ^ 1);
 
     const int kt0 = t * BN;
-    if (active && kt0 < khi && kt0 + BN > klo) {
+    // One tile of work: S^T, optional mask, softmax, PV. Instantiated twice so
+    // the common unmasked tile never merges with the masked one (no register
+    // copies of the S accumulators at a join).
+    auto tile = [&](auto masked) {
+      constexpr bool MASK = decltype(masked)::value;
       const char* sK = smem + buf * STAGE;
       const char* sV = sK + TILE;
 
+      // ---- S^T = K . Q^T: K fragments read one step ahead of the MFMAs ----
       f32x16 sacc[NKB];
+      bf16x8 kf[NKB], kn[NKB];
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
+        kf[kb] = *reinterpret_cast<const bf16x8*>(sK + kb * 32 * ROW + koff[0]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-        const int krow = kb * 32 + lq;
+      }
 #pragma unroll
-        for (int st = 0; st < D / 16; ++st) {
-          bf16x8 a = *reinterpret_cast<const bf16x8*>(sK + krow * ROW + (((2 * st + hf) ^ (krow & 7)) << 4));
-          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, qreg[st]), sacc[kb], 0, 0, 0);
+      for (int st = 0; st < D / 16; ++st) {
+        if (st + 1 < D / 16) {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+            kn[kb] = *reinterpret_cast<const bf16x8*>(sK + kb * 32 * ROW + koff[st + 1]);
         }
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], __builtin_bit_cast(bf16x8, qreg[st]), sacc[kb], 0, 0, 0);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) kf[kb] = kn[kb];
       }
 
-      const bool need_mask =
-          (kt0 + BN > T) || (p.causal && kt0 + BN - 1 > r0) ||
-          (p.window >= 0 && (rlast - kt0 > p.window || kt0 + BN - 1 - r0 > p.window));
-      if (need_mask) {
+      if constexpr (MASK) {
         const int qi = r0 + lq;
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
@@ -196,32 +224,43 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
             bool ok = kj < T;
             if (p.causal) ok = ok && kj <= qi;
             if (p.window >= 0) ok = ok && abs(qi - kj) <= p.window;
-            if (!ok) sacc[kb][r] = -INFINITY;
+            sacc[kb][r] = ok ? sacc[kb][r] : -INFINITY;
           }
       }
 
-      float mx = -INFINITY;
+      // ---- row max (v_maximum3: no NaN canonicalisation), across halves ----
+      float mx4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-      mx = fmaxf(mx, wave_xor32(mx));
-      const float m_new = fmaxf(m_i, mx * c2);
-      const float base = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_i - base);
-      m_i = m_new;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+        for (int r = 0; r < 16; r += 2)
+          mx4[(kb * 8 + r / 2) & 3] = __builtin_elementwise_maximum(
+              mx4[(kb * 8 + r / 2) & 3], __builtin_elementwise_maximum(sacc[kb][r], sacc[kb][r + 1]));
+      float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx4[0], mx4[1]),
+                                               __builtin_elementwise_maximum(mx4[2], mx4[3]));
+      mx = __builtin_elementwise_maximum(mx, wave_xor32(mx)) * c2;
+
+      // Lazy rescaling: the reference max moves only when a row's max grows
+      // by more than 2^8 (P then stays <= 256, exact range for fp16).
+      if (__builtin_amdgcn_ballot_w64(mx > m_i + 8.0f)) {
+        const float m_new = __builtin_elementwise_maximum(m_i, mx);
+        // m_i = -inf: nothing accumulated yet, alpha = 0 (and no -inf - -inf)
+        const float alpha = __builtin_amdgcn_exp2f(m_i - (m_new == -INFINITY ? 0.f : m_new));
+        m_i = m_new;
         l_i *= alpha;
 #pragma unroll
         for (int i = 0; i < NDB; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
       }
+      const float base = (m_i == -INFINITY) ? 0.f : m_i;
 
-      f16x8 pk[BN / 16];
+      // ---- P (fp16) per 16-key step, then O^T += V^T . P^T ----
       const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+      const char* vptr = sV + vbase_off;
 #pragma unroll
       for (int ks = 0; ks < BN / 16; ++ks) {
+        f16x8 pk;
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
           const float x0 = sacc[ks >> 1][8 * (ks & 1) + e];
@@ -229,31 +268,28 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
           f32x2 pr = {__builtin_amdgcn_exp2f(__builtin_fmaf(x0, c2, -base)),
                       __builtin_amdgcn_exp2f(__builtin_fmaf(x1, c2, -base))};
           f16x2 pair = __builtin_convertvector(pr, f16x2);
-          pk[ks][e] = pair[0];
-          pk[ks][e + 1] = pair[1];
+          pk[e] = pair[0];
+          pk[e + 1] = pair[1];
           l_i = __builtin_amdgcn_fdot2(pair, ones, l_i, false);
         }
-      }
-
-      // O^T += V^T . P^T; A operand = two transposed 4-key reads per lane.
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const int col = db * 32 + 16 * (g16 & 1) + 4 * (j16 & 3);
-#pragma unroll
-        for (int ks = 0; ks < BN / 16; ++ks) {
-          const int row1 = ks * 16 + 4 * hf + (j16 >> 2);
-          const int row2 = row1 + 8;
-          const int off1 = vswz<D>(row1, col >> 3) + (col & 7) * 2;
-          const int off2 = vswz<D>(row2, col >> 3) + (col & 7) * 2;
-          s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4*)(sV + off1));
-          s16x4 a2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4*)(sV + off2));
+        for (int db = 0; db < NDB; ++db) {
+          const char* vp = vptr + ks * 16 * VROWB + db * 64;
+          s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vp));
+          s16x4 a2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vp + 8 * VROWB));
           f16x4 h1 = __builtin_bit_cast(f16x4, a1), h2 = __builtin_bit_cast(f16x4, a2);
           f16x8 a = {h1[0], h1[1], h1[2], h1[3], h2[0], h2[1], h2[2], h2[3]};
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pk[ks], oacc[db], 0, 0, 0);
+          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pk, oacc[db], 0, 0, 0);
         }
       }
+    };
+
+    if (active && kt0 < khi && kt0 + BN > klo) {
+      const bool need_mask =
+          (kt0 + BN > T) || (p.causal && kt0 + BN - 1 > r0) ||
+          (p.window >= 0 && (rlast - kt0 > p.window || kt0 + BN - 1 - r0 > p.window));
+      if (need_mask) tile(std::true_type{});
+      else tile(std::false_type{});
     }
 
     if (more) store_v(buf ^ 1);
@@ -262,7 +298,7 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
   }
 
   if (!active || qrow >= T) return;
-  const float l_tot = l_i + wave_xor32(l_i);
+  const float l_tot = wave_sum_halves(l_i);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   char* orow = p.o + ((int64_t)(seg + qrow) * p.o_stride + (int64_t)head * D) * (p.out_bf16 ? 2 : 4);
 #pragma unroll
@@ -287,11 +323,14 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
 
 }  // namespace
 
+template <int D, int BN>
+constexpr int fast_lds() { return 2 * (BN * D * 2 + BN * vrow_bytes<D>()); }
+
 bool bf16_fast_kernel(int d, AttnKernelFn* fn, int* bn, int* nw, int* lds) {
   switch (d) {
-    case 64: *fn = attn_bf16_kernel<64, 64, 4>; *bn = 64; *nw = 4; *lds = 2 * 2 * 64 * 64 * 2; return true;
-    case 128: *fn = attn_bf16_kernel<128, 64, 4>; *bn = 64; *nw = 4; *lds = 2 * 2 * 64 * 128 * 2; return true;
-    case 256: *fn = attn_bf16_kernel<256, 64, 4>; *bn = 64; *nw = 4; *lds = 2 * 2 * 64 * 256 * 2; return true;
+    case 64: *fn = attn_bf16_kernel<64, 64, 4>; *bn = 64; *nw = 4; *lds = fast_lds<64, 64>(); return true;
+    case 128: *fn = attn_bf16_kernel<128, 64, 4>; *bn = 64; *nw = 4; *lds = fast_lds<128, 64>(); return true;
+    case 256: *fn = attn_bf16_kernel<256, 64, 4>; *bn = 64; *nw = 4; *lds = fast_lds<256, 64>(); return true;
     default: return false;
   }
 }
