@@ -421,11 +421,12 @@ struct KernelCfg {
   int bn;       // keys per tile
   int nw;       // waves per workgroup
   int lds;      // dynamic LDS bytes
+  int rows;     // query rows per wave (32 or 64)
 };
 
 template <typename E, int D, int BN, int NW, bool PV16>
 KernelCfg make_cfg() {
-  return KernelCfg{attn_fwd_kernel<E, D, BN, NW, PV16>, D, BN, NW, 4 * BN * D * (int)sizeof(E)};
+  return KernelCfg{attn_fwd_kernel<E, D, BN, NW, PV16>, D, BN, NW, 4 * BN * D * (int)sizeof(E), 32};
 }
 
 // `fits32`: every text's q/k/v rows span < 4 GiB, as the fast kernel's
@@ -436,7 +437,7 @@ int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, bool fits32, K
     AttnKernelFn fn;
     int bn, nw, lds;
     if (bf16_fast_kernel(head_dim, &fn, &bn, &nw, &lds)) {
-      *cfg = KernelCfg{fn, head_dim, bn, nw, lds};
+      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32};
       return INL_OK;
     }
   }
@@ -522,7 +523,7 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
   if (rc) return rc;
   const int group = d->h_q / d->h_kv;
   s->hpw = heads_per_wg(group, s->cfg.nw);
-  s->block_m = 32 * (s->cfg.nw / s->hpw);
+  s->block_m = s->cfg.rows * (s->cfg.nw / s->hpw);
   const int BM = s->block_m, BN = s->cfg.bn;
   struct Tmp { int4 it; int cost; };
   std::vector<Tmp> tmp;

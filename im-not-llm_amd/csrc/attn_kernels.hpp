@@ -16,7 +16,7 @@ struct AttnParams {
   int32_t groups_per_kv;  // (h_q / h_kv) / hpw
   int32_t group;      // h_q / h_kv
   int32_t hpw;        // query heads per workgroup
-  int32_t rb;         // 32-row blocks per head per workgroup (NW / hpw)
+  int32_t rb;         // waves per head per workgroup (NW / hpw), 32 rows each
   int32_t head_dim;
   int32_t causal;
   int32_t window;

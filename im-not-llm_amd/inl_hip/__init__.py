@@ -58,8 +58,7 @@ ATTN_PV_BF16 = 1
 
 class NormRopeDesc(ctypes.Structure):
     _fields_ = [
-        ("n_texts", c_i32),
-        ("cu_seqlens_host", ctypes.POINTER(c_i32)),
+        ("n_tokens", c_i64),
         ("heads", c_i32),
         ("head_dim", c_i32),
         ("x_row_stride", c_i64),
@@ -101,6 +100,21 @@ _varlen_fwd = _sig("inl_attn_varlen_fwd", ctypes.c_int, ctypes.POINTER(AttnDesc)
                    c_void_p)
 
 
+_norm_rope = _sig("inl_norm_rope_fwd", ctypes.c_int, ctypes.POINTER(NormRopeDesc), c_void_p,
+                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p)
+_rope_table = _sig("inl_rope_table_host", ctypes.c_int, c_i32, ctypes.c_double, c_i32, c_i32,
+                   c_void_p, c_void_p)
+_positions = _sig("inl_positions_host", ctypes.c_int, c_i32, c_void_p, c_void_p)
+_pool_last = _sig("inl_pool_last_fwd", ctypes.c_int, c_i32, c_void_p, c_i32, c_i64, c_i32,
+                  c_void_p, c_void_p, ctypes.c_float, c_i32, c_void_p, c_void_p)
+_pool_mean = _sig("inl_pool_mean_fwd", ctypes.c_int, c_i32, c_void_p, c_i32, c_i64, c_i32,
+                  c_void_p, c_i32, c_void_p, c_void_p)
+_l2 = _sig("inl_l2_normalize_fwd", ctypes.c_int, c_i32, c_i32, c_i64, c_void_p, c_i64,
+           c_void_p, ctypes.c_float, c_i32, c_void_p)
+_splade = _sig("inl_pool_splade_fwd", ctypes.c_int, c_i32, c_void_p, c_i32, c_void_p, c_i64,
+               c_void_p, ctypes.c_float, c_void_p, c_i32, c_void_p, c_i32, c_void_p, c_void_p)
+
+
 class InlError(RuntimeError):
     """A non-zero status from the library, with its message."""
 
@@ -132,7 +146,7 @@ def exported_symbols() -> list:
     names = []
     for n in ("inl_attn_plan_create", "inl_attn_plan_destroy", "inl_attn_plan_info",
               "inl_attn_fwd", "inl_attn_workspace_size", "inl_attn_varlen_fwd",
-              "inl_norm_rope_fwd", "inl_rope_table_host", "inl_pool_last_fwd",
+              "inl_norm_rope_fwd", "inl_rope_table_host", "inl_positions_host", "inl_pool_last_fwd",
               "inl_pool_mean_fwd", "inl_l2_normalize_fwd", "inl_pool_splade_fwd",
               "inl_last_error", "inl_abi_version"):
         if getattr(_lib, n, None) is not None:
@@ -268,3 +282,109 @@ def attention_flops(lengths, h_q, head_dim, causal, window=-1) -> int:
                     hi = min(hi, qi + 1)
                 total += hi - max(0, qi - w)
     return 4 * h_q * head_dim * total
+
+
+# ---------------------------------------------------------------------------
+# Prologue
+# ---------------------------------------------------------------------------
+
+def rope_table(rotary_dim: int, theta: float, positions: int, mode: int = 0):
+    """(cos, sin) float32 numpy arrays ``[positions, rotary_dim/2]`` built by
+    the library exactly as the reference builds them (mode 0: f64 angles;
+    mode 1: f32, the Qwen3.5 table)."""
+    import numpy as np
+    half = rotary_dim // 2
+    c = np.empty((positions, half), dtype=np.float32)
+    s_ = np.empty((positions, half), dtype=np.float32)
+    _check(_rope_table(rotary_dim, float(theta), positions, mode, c.ctypes.data, s_.ctypes.data))
+    return c, s_
+
+
+def positions(cu_seqlens):
+    """Text-local positions (int32 numpy) of the packed tokens."""
+    import numpy as np
+    cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+    out = np.empty(int(cu[-1]) if len(cu) else 0, dtype=np.int32)
+    _check(_positions(len(cu) - 1, cu.ctypes.data, out.ctypes.data))
+    return out
+
+
+def norm_rope(x, rows=None, cos=None, sin=None, *, weight=None, eps=1e-6, norm=True,
+              rotary_dim=None, sections=1, cos2=None, sin2=None, out=None, out_dtype=None,
+              round_tables=False, round_norm=False, stream=None):
+    """Fused per-head RMSNorm + RoPE over ``x [N, heads, head_dim]`` (torch
+    device tensor; token rows may be strided). ``rows`` (int32 device [N]) is
+    the table row of each token; ``cos``/``sin`` are f32 device tables.
+    ``rotary_dim=0`` (or no tables) skips the rope."""
+    import torch
+    n, heads, hd = x.shape
+    od = out_dtype if out_dtype is not None else x.dtype
+    if out is None:
+        out = torch.empty((n, heads, hd), dtype=od, device=x.device)
+    rd = (hd if cos is not None else 0) if rotary_dim is None else rotary_dim
+    d = NormRopeDesc()
+    d.n_tokens, d.heads, d.head_dim = n, heads, hd
+    d.x_row_stride, d.y_row_stride = x.stride(0), out.stride(0)
+    d.dtype, d.out_dtype = _dtype_code(x.dtype), _dtype_code(out.dtype)
+    d.norm, d.eps = int(bool(norm)), float(eps)
+    d.rotary_dim, d.sections = int(rd), int(sections)
+    d.table_rows = int(cos.shape[0]) if cos is not None else 0
+    d.round_tables, d.round_norm = int(bool(round_tables)), int(bool(round_norm))
+    ptr = lambda t: t.data_ptr() if t is not None else None
+    _check(_norm_rope(ctypes.byref(d), x.data_ptr(), out.data_ptr(), ptr(weight), ptr(rows),
+                      ptr(cos), ptr(sin), ptr(cos2), ptr(sin2), _stream_ptr(stream)))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Epilogues (``cu`` is an int32 device tensor of packed row offsets)
+# ---------------------------------------------------------------------------
+
+def pool_last(hidden, cu, *, weight=None, eps=1e-6, round_norm=False, stream=None):
+    import torch
+    n_texts = cu.numel() - 1
+    out = torch.empty((n_texts, hidden.shape[1]), dtype=torch.float32, device=hidden.device)
+    _check(_pool_last(n_texts, cu.data_ptr(), hidden.shape[1], hidden.stride(0),
+                      _dtype_code(hidden.dtype), hidden.data_ptr(),
+                      weight.data_ptr() if weight is not None else None, float(eps),
+                      int(bool(round_norm)), out.data_ptr(), _stream_ptr(stream)))
+    return out
+
+
+def pool_mean(hidden, cu, *, normalize=False, stream=None):
+    import torch
+    n_texts = cu.numel() - 1
+    out = torch.empty((n_texts, hidden.shape[1]), dtype=torch.float32, device=hidden.device)
+    _check(_pool_mean(n_texts, cu.data_ptr(), hidden.shape[1], hidden.stride(0),
+                      _dtype_code(hidden.dtype), hidden.data_ptr(), int(bool(normalize)),
+                      out.data_ptr(), _stream_ptr(stream)))
+    return out
+
+
+def l2_normalize(x, dim=None, *, eps_inside=1e-12, skip_zero=False, out=None, stream=None):
+    import torch
+    rows, width = x.shape
+    dim = width if dim is None else dim
+    if out is None:
+        out = torch.empty((rows, dim), dtype=torch.float32, device=x.device)
+    _check(_l2(rows, dim, x.stride(0), x.data_ptr(), out.stride(0), out.data_ptr(),
+               float(eps_inside), int(bool(skip_zero)), _stream_ptr(stream)))
+    return out
+
+
+def pool_splade(logits, offs, *, bias=None, shift=0.0, masked_ids=(), canonical=None,
+                out_dim=None, stream=None):
+    """SPLADE pooling over bias-free f32 logits ``[n_speak, vocab]`` with
+    speaking-position offsets ``offs`` (int32 device [rows+1])."""
+    import torch
+    rows = offs.numel() - 1
+    vocab = logits.shape[1]
+    if out_dim is None:
+        out_dim = vocab if canonical is None else int(canonical.max().item()) + 1
+    out = torch.empty((rows, out_dim), dtype=torch.float32, device=logits.device)
+    m = (c_i32 * max(1, len(masked_ids)))(*[int(v) for v in masked_ids])
+    _check(_splade(rows, offs.data_ptr(), vocab, logits.data_ptr(), logits.stride(0),
+                   bias.data_ptr() if bias is not None else None, float(shift), m,
+                   len(masked_ids), canonical.data_ptr() if canonical is not None else None,
+                   out_dim, out.data_ptr(), _stream_ptr(stream)))
+    return out

@@ -5,7 +5,7 @@
  * that im-not-llm's Rust engines can bind it over FFI and wrap it as a candle
  * custom op. Every pointer named `q`, `k`, `v`, `out`, `x`, `y`, `hidden`,
  * `logits`, `pooled`, `cos`, `sin`, `weight`, `bias`, `canonical`, `rows`,
- * `ends` is a device pointer; `cu_seqlens_host` and `lengths_host` are host
+ * `cu`, `offs` is a device pointer; names ending in `_host` are host
  * pointers. Work is enqueued on `stream` (a hipStream_t; NULL = the null
  * stream) and is asynchronous unless a function says otherwise.
  *
@@ -125,39 +125,47 @@ int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q,
  *   norm:  x / sqrt(mean(x^2) + eps) * weight   (weight NULL = all ones;
  *          norm == 0 skips the norm);
  *   rope:  sections == 1: the first rotary_dim features are rotated in
- *          half-split pairs (i, i + rotary_dim/2) with cos/sin row `pos`,
- *          where pos = the row's position inside its text; the rest pass
- *          through. sections == 2 (axial): each half of the head is rotated
- *          by its own half-split with tables cos/sin (first half) and
- *          cos2/sin2 (second half), indexed by the packed token row.
+ *          half-split pairs (i, i + rotary_dim/2) with cos/sin row
+ *          rows[token] (the token's position inside its text; positions
+ *          restart at 0 per packed text); the rest pass through.
+ *          sections == 2 (axial): each half of the head is rotated by its
+ *          own half-split, the first half with cos/sin, the second with
+ *          cos2/sin2, tables indexed by rows[token] (per-token tables).
  *          rotary_dim == 0 skips the rope.
- * Tables are f32 `[rows, table_width]`; with round_tables=1 every table value
- * is rounded to bf16 first (the reference stores them in the model dtype).
- * With round_norm=1 the normalised value is rounded to the output dtype
- * before the rotation (the reference materialises it in the model dtype).
+ * Tables are f32 `[table_rows, rotary_dim / 2]` (sections 1) or
+ * `[table_rows, head_dim / 4]` (sections 2). A row index outside
+ * [0, table_rows) yields NaN for that token instead of an out-of-range read.
+ * round_tables = 1 rounds table values to bf16 (the reference stores tables
+ * in the model dtype); round_norm = 1 rounds the normalised value to the
+ * output dtype before the rotation (the reference materialises it).
+ * In-place operation (y == x, same strides) is allowed.
  * --------------------------------------------------------------------- */
 typedef struct inl_norm_rope_desc {
-  int32_t n_texts;
-  const int32_t* cu_seqlens_host; /* [n_texts + 1] */
+  int64_t n_tokens;
   int32_t heads;
-  int32_t head_dim;               /* even, <= 512 */
-  int64_t x_row_stride;           /* 0 = heads*head_dim */
-  int64_t y_row_stride;           /* 0 = heads*head_dim */
+  int32_t head_dim;               /* multiple of 8, <= 512 */
+  int64_t x_row_stride;           /* elements; 0 = heads*head_dim */
+  int64_t y_row_stride;           /* elements; 0 = heads*head_dim */
   int32_t dtype;                  /* x dtype */
   int32_t out_dtype;              /* y dtype */
   int32_t norm;                   /* 1 = apply the RMSNorm */
   float eps;
-  int32_t rotary_dim;             /* 0 = no rope; sections==1: even <= head_dim */
+  int32_t rotary_dim;             /* 0 = no rope; sections 1: multiple of 16 <= head_dim */
   int32_t sections;               /* 1 = half-split, 2 = axial */
-  int32_t table_rows;             /* rows in cos/sin (positions or tokens) */
+  int32_t table_rows;
   int32_t round_tables;
   int32_t round_norm;
 } inl_norm_rope_desc;
 
-int inl_norm_rope_fwd(const inl_norm_rope_desc* desc, const void* x,
-                      void* y, const void* weight /* [head_dim] dtype or NULL */,
+int inl_norm_rope_fwd(const inl_norm_rope_desc* desc, const void* x, void* y,
+                      const void* weight /* [head_dim], dtype, or NULL */,
+                      const int32_t* rows /* [n_tokens] device, table row per token */,
                       const float* cos, const float* sin,
                       const float* cos2, const float* sin2, void* stream);
+
+/* Host helper: text-local positions of packed tokens (0..len-1 per text),
+ * written to a host array of cu_seqlens_host[n_texts] entries. */
+int inl_positions_host(int32_t n_texts, const int32_t* cu_seqlens_host, int32_t* positions);
 
 /* Host helper: RoPE tables as the reference builds them.
  * mode 0: inv_freq and angles in f64, stored f32 (qwen3/mod.rs:131-153,
@@ -167,44 +175,49 @@ int inl_rope_table_host(int32_t rotary_dim, double theta, int32_t positions,
                         int32_t mode, float* cos_out, float* sin_out);
 
 /* ------------------------------------------------------------------------
- * Epilogues
+ * Epilogues. `cu` is a DEVICE int32 array [n_texts + 1] of packed row
+ * offsets (cu[0] == 0, nondecreasing); outputs are f32.
  * --------------------------------------------------------------------- */
 
 /* Last-token pooling: pooled[b] = l2(rms_norm(hidden[cu[b+1]-1]) * weight),
- * f32 output [n_texts, hidden_dim]. Replaces qwen3/mod.rs:356-357 + :464-469.
- * round_norm=1 rounds the normed row to `dtype` before the L2 (the reference
- * keeps it in the model dtype). Empty texts yield zero rows. */
-int inl_pool_last_fwd(int32_t n_texts, const int32_t* cu_seqlens_host,
-                      int32_t hidden_dim, int64_t row_stride, int32_t dtype,
-                      const void* hidden, const void* weight, float eps,
-                      int32_t round_norm, float* pooled, void* stream);
+ * [n_texts, hidden_dim]. Replaces the final norm of the last position and
+ * the L2 normalisation of crates/inl-text/src/qwen3/mod.rs:356-357, 464-469
+ * (l2: x / sqrt(sum x^2 + 1e-12)). round_norm = 1 rounds the normed row to
+ * bf16 before the L2 (the reference keeps it in the model dtype). Empty
+ * texts yield zero rows. weight NULL = all ones. */
+int inl_pool_last_fwd(int32_t n_texts, const int32_t* cu, int32_t hidden_dim,
+                      int64_t row_stride, int32_t dtype, const void* hidden,
+                      const void* weight, float eps, int32_t round_norm,
+                      float* pooled, void* stream);
 
-/* Mean pooling: pooled[b] = sum_{rows of b} hidden / len_b, f32 output
- * [n_texts, hidden_dim] (gemma2.rs:647-656). normalize=1 also L2-normalises
- * (gemma2.rs:660-661, when the projection is the identity). */
-int inl_pool_mean_fwd(int32_t n_texts, const int32_t* cu_seqlens_host,
-                      int32_t hidden_dim, int64_t row_stride, int32_t dtype,
-                      const void* hidden, int32_t normalize, float* pooled,
-                      void* stream);
+/* Mean pooling: pooled[b] = sum of the rows of text b / len_b,
+ * [n_texts, hidden_dim] (crates/inl-text/src/gemma2.rs:647-656); empty texts
+ * give zeros. normalize = 1 also L2-normalises each row with 1e-12 inside
+ * the square root (gemma2.rs:660-661, for an identity projection). */
+int inl_pool_mean_fwd(int32_t n_texts, const int32_t* cu, int32_t hidden_dim,
+                      int64_t row_stride, int32_t dtype, const void* hidden,
+                      int32_t normalize, float* pooled, void* stream);
 
-/* Row-wise L2 normalisation of the first `dim` entries of f32 rows (in
- * place allowed): x / sqrt(sum x^2 + eps_inside). eps_inside = 1e-12 is the
+/* Row-wise L2 normalisation of the first `dim` entries of f32 rows (in place
+ * allowed): x / sqrt(sum x^2 + eps_inside). eps_inside = 1e-12 is the
  * pooled-embedding norm (qwen3/mod.rs:468); eps_inside = 0 with
- * skip_zero = 1 is Matryoshka truncate-and-renormalise
- * (crates/inl-text/src/native.rs:822-830). */
+ * skip_zero = 1 is the Matryoshka truncate-and-renormalise of
+ * crates/inl-text/src/native.rs:822-830 (rows of norm 0 are left as is). */
 int inl_l2_normalize_fwd(int32_t rows, int32_t dim, int64_t in_stride,
                          const float* x, int64_t out_stride, float* y,
                          float eps_inside, int32_t skip_zero, void* stream);
 
 /* SPLADE pooling (crates/inl-sparse/src/modernbert.rs:806-907):
- *   m[r, t]  = max over speaking positions p in [ends[r-1], ends[r]) of
- *              logits[p, t]   (f32 [n_speak, vocab], bias-free);
- *   w[r, t]  = ln(relu(m + bias[t] - shift) * open[t] + 1), open[t] = 0 for
- *              t in masked_ids, -inf max (no speaker) gives 0;
- *   out[r,c] = max(0, max over t with canonical[t] == c of w[r, t])
- *              (canonical NULL: out = w, out_dim == vocab).
- * ends_host: [rows] host, exclusive ends. out: f32 [rows, out_dim]. */
-int inl_pool_splade_fwd(int32_t rows, const int64_t* ends_host, int32_t vocab,
+ *   m[r, t]   = max over speaking positions p in [offs[r], offs[r+1]) of
+ *               logits[p, t]  (f32, bias-free; -inf if the row has none);
+ *   w[r, t]   = ln(relu(m + bias[t] - shift) * open[t] + 1), open[t] = 0 for
+ *               the masked vocabulary ids (at most 16);
+ *   out[r, c] = max(0, max over t with canonical[t] == c of w[r, t])
+ *               (canonical NULL: out = w and out_dim == vocab).
+ * offs: DEVICE int32 [rows + 1]. bias NULL = no bias. out: [rows, out_dim].
+ * The max and the fold do not depend on evaluation order: for given logits
+ * the output, and its active-term set {c : out > 0}, is bit-exact. */
+int inl_pool_splade_fwd(int32_t rows, const int32_t* offs, int32_t vocab,
                         const float* logits, int64_t logits_stride,
                         const float* bias, float shift,
                         const int32_t* masked_ids_host, int32_t n_masked,
