@@ -11,10 +11,16 @@ before timing, as an engine builds one per batch and reuses it for every
 layer).
 
 Prints one JSON line: tokens/s (value), attention TFLOP/s, the roofline of
-the attention kernel (algorithmic FLOPs / kernel time from HIP events on the
-launch stream, against the 2516.6 TFLOP/s bf16 dense MFMA peak) and the CPU
-baseline (the oracle's multi-threaded f32 C restatement of the reference
-CPU flash path, timed on a bounded sample of the same workload).
+the attention kernel and the CPU baseline. The roofline divides the
+algorithmic work of one launch (FLOPs: 4 * head_dim per visible (q, k) pair
+per query head; HBM bytes: Q, K, V read once and O written once) by the
+average launch time from HIP events on the launch stream, against the
+2516.6 TFLOP/s bf16 dense MFMA peak and 8 TB/s of HBM; `bound` names the
+one with the larger floor on time, and `traffic` is the measured HBM bytes
+per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary for
+the workload. The CPU baseline is the oracle's multi-threaded f32 C
+restatement of the reference CPU flash path, timed on a bounded sample of
+the same workload.
 
 Other workloads (--workload): gemma_window, gemma_full, modernbert_local,
 modernbert_global, vision, pplx_causal - reported the same way.
@@ -97,13 +103,17 @@ def make_inputs(lengths, hq, hkv, d, scale, seed, torch, dev):
 
 
 def cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale, seconds):
-    """The oracle's f32 C restatement on host cores over consecutive batches
-    of the same workload until `seconds` of work (at least one batch)."""
+    """The oracle's f32 C restatement on host cores over the workload's
+    batches in order, wrapping round, until `seconds` of work (at least one
+    batch)."""
     from oracle import cref, attention as oa
     cref.lib()
+    host = [tuple(t.float().cpu().numpy() for t in qkv) for qkv in inputs]
     tokens, flops, spent, used = 0, 0, 0.0, 0
-    for lens, (q, k, v) in zip(batches, inputs):
-        qh, kh, vh = (t.float().cpu().numpy() for t in (q, k, v))
+    while spent < seconds:
+        i = used % len(batches)
+        lens = batches[i]
+        qh, kh, vh = host[i]
         cu = oa.cu_from_lengths(lens)
         t0 = time.perf_counter()
         cref.attention_f32(qh, kh, vh, cu, causal=causal, window=window, scale=scale)
@@ -111,16 +121,14 @@ def cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale, seconds):
         tokens += int(sum(lens))
         flops += oa.attention_flops(lens, hq, d, causal, window)
         used += 1
-        if spent >= seconds:
-            break
     return {
         "value": round(tokens / spent, 1),
         "unit": "tokens/s",
         "cores": cref.threads(),
         "kind": "port",
-        "sample": (f"first {used} of {len(batches)} batches ({tokens} tokens, "
-                   f"{flops / 1e12:.4f} TFLOP) through oracle/attn_ref.c (f32 per-text online-softmax "
-                   f"attention, OpenMP), {spent:.2f} s"),
+        "sample": (f"{used} batch launches ({used / len(batches):.2f} passes over the {len(batches)} batches; "
+                   f"{tokens} tokens, {flops / 1e12:.4f} TFLOP) through oracle/attn_ref.c (f32 per-text "
+                   f"online-softmax attention, OpenMP), {spent:.2f} s"),
         "tflops": round(flops / spent / 1e12, 4),
     }
 
@@ -136,6 +144,19 @@ def read_traffic(name: str):
     return None
 
 
+def roofline(hbm_bound, tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch):
+    """The attention kernel against its binding roofline, the other beside it."""
+    mfma = {"achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
+    hbm = {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+           "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    main_, other = (hbm, mfma) if hbm_bound else (mfma, hbm)
+    return {"bound": "hbm" if hbm_bound else "mfma", **main_, "traffic": traffic,
+            "kernel": kernel, "avg_launch_us": round(avg_ms * 1e3, 2),
+            "algorithmic_per_launch": {"flop": flop_launch, "hbm_bytes": bytes_launch},
+            "other": {"bound": "mfma" if hbm_bound else "hbm", **other}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,7 +165,21 @@ def main():
     ap.add_argument("--workload", default="qwen3")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run device-to-device copies of MIB MiB (3 launches): the known-size "
+                         "reference that scales the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.randn(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 3}))
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -167,6 +202,11 @@ def main():
         outs.append(torch.empty_like(q))
     tokens = sum(sum(b) for b in batches)
     flops = sum(attention_flops(b, hq, d, causal, window) for b in batches)
+    # algorithmic HBM bytes: Q, K, V read once and O written once, bf16
+    hbm_bytes = tokens * (2 * hq * d + 2 * 2 * hkv * d + 2 * hq * d)
+    bn = plans[0].info()["block_n"]
+    kernel = (f"attn_bf16_kernel<{d}, {bn}, 4>" if d in (64, 128, 256)
+              else f"attn_fwd_kernel<bf16, {d}, {bn}>")
     n_launch = len(batches)
     stream = torch.cuda.current_stream()
     log(f"workload: {label}; {flops / 1e12:.4f} TFLOP per step, {n_launch} launches")
@@ -195,6 +235,10 @@ def main():
     kernel_ms = sum(a.elapsed_time(b) for ev in events for a, b in ev)
     avg_launch_ms = kernel_ms / (args.steps * n_launch)
     achieved = flops / n_launch / (avg_launch_ms * 1e-3) / 1e12
+    achieved_gbs = hbm_bytes / n_launch / (avg_launch_ms * 1e-3) / 1e9
+    # the binding roofline is the one with the larger lower bound on time
+    mfma_floor = flops / (PEAK_BF16_TFLOPS * 1e12)
+    hbm_floor = hbm_bytes / (PEAK_HBM_GBS * 1e9)
     tok_s = tokens * args.steps / wall
     traffic = read_traffic(args.workload)
     log(f"wall {wall:.4f} s for {args.steps} steps; kernel {kernel_ms:.3f} ms; "
@@ -217,16 +261,8 @@ def main():
                    "attention_tflop_per_step": round(flops / 1e12, 6)},
         "attention_tflops": round(flops * args.steps / wall / 1e12, 2),
         "attention_frac_of_peak": round(flops * args.steps / wall / 1e12 / PEAK_BF16_TFLOPS, 4),
-        "roofline": {
-            "bound": "mfma",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": traffic,
-            "kernel": "attn_fwd_kernel<bf16, D=128, BN=64, NW=4, PV16>",
-            "avg_launch_us": round(avg_launch_ms * 1e3, 2),
-        },
+        "roofline": roofline(hbm_floor >= mfma_floor, achieved, achieved_gbs, traffic, kernel,
+                             avg_launch_ms, flops / n_launch, hbm_bytes / n_launch),
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale,
