@@ -499,6 +499,18 @@ int validate_desc(const inl_attn_desc* d, int64_t* total_tokens) {
   for (int b = 0; b < d->n_texts; ++b)
     if (d->cu_seqlens_host[b + 1] - d->cu_seqlens_host[b] >= (1 << 16) * 32)
       return fail(INL_E_UNSUPPORTED, "attention: a text longer than 2^21 tokens");
+  if (d->seq_starts_host) {
+    int64_t rows = 0;
+    for (int b = 0; b < d->n_texts; ++b) {
+      const int64_t st = d->seq_starts_host[b];
+      const int64_t end = st + (d->cu_seqlens_host[b + 1] - d->cu_seqlens_host[b]);
+      if (st < 0 || end > INT32_MAX)
+        return fail(INL_E_INVALID, "attention: seq_starts_host[b] must be >= 0 and the text must end "
+                                   "below row 2^31");
+      rows = std::max(rows, end);
+    }
+    *total_tokens = rows;
+  }
   return INL_OK;
 }
 
@@ -528,8 +540,8 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
   struct Tmp { int4 it; int cost; };
   std::vector<Tmp> tmp;
   for (int b = 0; b < d->n_texts; ++b) {
-    const int seg = d->cu_seqlens_host[b];
-    const int T = d->cu_seqlens_host[b + 1] - seg;
+    const int seg = d->seq_starts_host ? d->seq_starts_host[b] : d->cu_seqlens_host[b];
+    const int T = d->cu_seqlens_host[b + 1] - d->cu_seqlens_host[b];
     for (int q0 = 0; q0 < T; q0 += BM) {
       const int qlast = std::min(q0 + BM, T) - 1;
       int lo = 0, hi = d->causal ? qlast + 1 : T;
@@ -602,7 +614,7 @@ int check_ptrs(const void* q, const void* k, const void* v, const void* out, int
 }  // namespace inl
 
 struct inl_attn_plan {
-  inl_attn_desc desc;     // cu_seqlens_host is not kept
+  inl_attn_desc desc;     // cu_seqlens_host and seq_starts_host are not kept
   inl::Schedule sched;    // items also kept on the host for inspection
   int4* d_items = nullptr;
   int64_t total_tokens = 0;
@@ -619,6 +631,7 @@ extern "C" int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** p
   if (!pl) return fail(INL_E_NOMEM, "attention: host allocation failed");
   pl->desc = *desc;
   pl->desc.cu_seqlens_host = nullptr;
+  pl->desc.seq_starts_host = nullptr;
   pl->total_tokens = total;
   rc = build_schedule(desc, &pl->sched);
   if (rc) { delete pl; return rc; }

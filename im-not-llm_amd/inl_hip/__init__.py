@@ -50,6 +50,7 @@ class AttnDesc(ctypes.Structure):
         ("v_row_stride", c_i64),
         ("o_row_stride", c_i64),
         ("flags", c_i32),
+        ("seq_starts_host", ctypes.POINTER(c_i32)),
     ]
 
 
@@ -177,8 +178,10 @@ def _stream_ptr(stream) -> int:
 
 def make_attn_desc(cu_seqlens, h_q, h_kv, head_dim, *, causal, window=-1, scale=None,
                    dtype="bf16", out_dtype=None, q_row_stride=0, k_row_stride=0,
-                   v_row_stride=0, o_row_stride=0, flags=0):
-    """Build an ``AttnDesc``; the cu_seqlens array is kept alive on it."""
+                   v_row_stride=0, o_row_stride=0, flags=0, seq_starts=None):
+    """Build an ``AttnDesc``; the cu_seqlens (and seq_starts) arrays are kept
+    alive on it. ``seq_starts[b]`` is the first row of text b when texts are
+    not packed back to back (a padded batch); None = packed."""
     cu = _cu_array(cu_seqlens)
     codes = {"bf16": INL_BF16, "f32": INL_F32, INL_BF16: INL_BF16, INL_F32: INL_F32}
     d = AttnDesc()
@@ -194,6 +197,12 @@ def make_attn_desc(cu_seqlens, h_q, h_kv, head_dim, *, causal, window=-1, scale=
     d.v_row_stride, d.o_row_stride = int(v_row_stride), int(o_row_stride)
     d.flags = int(flags)
     d._cu_keepalive = cu
+    if seq_starts is not None:
+        if len(seq_starts) != d.n_texts:
+            raise ValueError(f"seq_starts must have {d.n_texts} entries, got {len(seq_starts)}")
+        st = _cu_array(seq_starts)
+        d.seq_starts_host = st
+        d._starts_keepalive = st
     return d
 
 
@@ -237,11 +246,13 @@ class AttnPlan:
 
 def varlen_attention(q, k, v, cu_seqlens, *, causal: bool, window: int = -1,
                      scale: Optional[float] = None, out_dtype=None, out=None,
-                     stream=None, flags: int = 0):
+                     stream=None, flags: int = 0, seq_starts=None):
     """Packed attention over torch device tensors ``q [N, Hq, D]``,
     ``k, v [N, Hkv, D]`` (token rows may be strided views of a fused QKV
     buffer). Returns ``out [N, Hq, D]``. Uses the one-shot C entry point
-    (``inl_attn_varlen_fwd``) with a workspace from torch's allocator."""
+    (``inl_attn_varlen_fwd``) with a workspace from torch's allocator.
+    ``seq_starts`` places text b at rows ``[seq_starts[b], seq_starts[b] +
+    len_b)`` (a padded batch); rows outside every text are not written."""
     import torch
     n, hq, d = q.shape
     hkv = k.shape[1]
@@ -252,7 +263,8 @@ def varlen_attention(q, k, v, cu_seqlens, *, causal: bool, window: int = -1,
     desc = make_attn_desc(cu_seqlens, hq, hkv, d, causal=causal, window=window, scale=scale,
                           dtype=dt, out_dtype="bf16" if out.dtype == torch.bfloat16 else "f32",
                           q_row_stride=q.stride(0), k_row_stride=k.stride(0),
-                          v_row_stride=v.stride(0), o_row_stride=out.stride(0), flags=flags)
+                          v_row_stride=v.stride(0), o_row_stride=out.stride(0), flags=flags,
+                          seq_starts=seq_starts)
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
         if t.stride(2) != 1 or t.stride(1) != d:
             raise InlError(-1, f"{name}: heads must be contiguous inside a token row")

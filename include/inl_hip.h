@@ -81,6 +81,15 @@ typedef struct inl_attn_desc {
   int64_t v_row_stride;            /* 0 = h_kv*head_dim */
   int64_t o_row_stride;            /* 0 = h_q*head_dim */
   int32_t flags;                   /* INL_ATTN_* bits, 0 = defaults */
+  /* Optional [n_texts]: the first row of text b in q, k, v and out (its
+   * length stays cu_seqlens_host[b+1] - cu_seqlens_host[b]). NULL = packed,
+   * text b starts at cu_seqlens_host[b]. With it a padded [B, T] batch runs
+   * in place: start b*T + pad_b for the left padding of
+   * crates/inl-core/src/attention.rs:126-199, b*T for the right padding of
+   * gemma2.rs:499-523 and modernbert.rs:594-617. Rows outside every text are
+   * not written (the reference leaves padded rows unspecified,
+   * attention.rs:213-214). */
+  const int32_t* seq_starts_host;
 } inl_attn_desc;
 
 /* bf16 inputs: the PV product runs in fp16 by default (V converted exactly

@@ -41,6 +41,9 @@ def test_attention_desc_validation_errors():
         (inl_hip.make_attn_desc(cu, 16, 8, 128, causal=True, scale=-1.0), -1, "scale"),
         (inl_hip.make_attn_desc(cu, 16, 8, 128, causal=True, q_row_stride=100), -1, "stride"),
         (inl_hip.make_attn_desc(cu, 16, 8, 128, causal=True, flags=8), -1, "flags"),
+        (inl_hip.make_attn_desc(cu, 16, 8, 128, causal=True, seq_starts=[-1, 0]), -1, "seq_starts"),
+        (inl_hip.make_attn_desc(cu, 16, 8, 128, causal=True, seq_starts=[0, 2**31 - 3]), -1,
+         "seq_starts"),
     ]
     for desc, code, word in cases:
         rc = inl_hip._ws_size(ctypes.byref(desc), ctypes.byref(n))
