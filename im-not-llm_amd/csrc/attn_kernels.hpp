@@ -42,4 +42,8 @@ __device__ __forceinline__ int swz(int r, int c, int row_bytes) {
 typedef void (*AttnKernelFn)(AttnParams);
 bool bf16_fast_kernel(int head_dim_padded, AttnKernelFn* fn, int* bn, int* nw, int* lds);
 
+// Ping-pong bf16 kernel (attn_pp.hip): 8 waves in two groups that alternate
+// MFMA and softmax phases; head dim 128.
+bool bf16_pp_kernel(int head_dim, AttnKernelFn* fn, int* bn, int* nw, int* lds);
+
 }  // namespace inl
