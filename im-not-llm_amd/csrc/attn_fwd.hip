@@ -303,7 +303,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-      mx = fmaxf(mx, wave_xor32(mx));
+      mx = half_max(mx);
       const float m_new = fmaxf(m_i, mx * c2);
       const float base = (m_new == -INFINITY) ? 0.f : m_new;
       const float alpha = __builtin_amdgcn_exp2f(m_i - base);
@@ -322,12 +322,12 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
       // ---- O^T += V^T . P^T ----
       if constexpr (ES == 2) {
         // P is rounded (fp16, or bf16 with INL_ATTN_PV_BF16) for the product;
-        // the row sum is taken over the same rounded values (dot2 against
-        // ones), so the weights that multiply V sum exactly to the normaliser.
+        // the row sum is taken over the same rounded values (in f32; the dot2
+        // instructions would wait for the matrix core), so the weights that
+        // multiply V sum exactly to the normaliser.
         typedef PT pt8 __attribute__((ext_vector_type(8)));
         typedef PT pt2 __attribute__((ext_vector_type(2)));
         pt8 pk[BN / 16];
-        const pt2 ones = {(PT)1.0f, (PT)1.0f};
 #pragma unroll
         for (int ks = 0; ks < BN / 16; ++ks) {
 #pragma unroll
@@ -336,8 +336,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             pt2 pair = __builtin_convertvector(pr, pt2);
             pk[ks][e] = pair[0];
             pk[ks][e + 1] = pair[1];
-            if constexpr (PV16) l_i = __builtin_amdgcn_fdot2(pair, ones, l_i, false);
-            else l_i = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l_i, false);
+            l_i += (float)pair[0] + (float)pair[1];
           }
         }
 #pragma unroll
@@ -384,7 +383,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
 
   // ---- epilogue: O = O^T / l, one query row per lane column ----
   if (!active || !qvalid) return;
-  const float l_tot = l_i + wave_xor32(l_i);
+  const float l_tot = half_sum(l_i);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   char* orow = p.o + ((int64_t)(seg + qrow) * p.o_stride + (int64_t)head * hd) * (p.out_bf16 ? 2 : 4);
 #pragma unroll

@@ -15,8 +15,8 @@
 //     is done by ALU instructions.
 //   - Buffer resources bound every text's rows: loads past the text return
 //     zero, so no load needs a branch.
-// The kernel requires head_dim == D (64, 128 or 256); other head dims take
-// the generic kernel.
+// The kernel serves head_dim 64 and 256 (128 takes the ping-pong kernel in
+// attn_pp.hip); other head dims take the generic kernel.
 
 #include <type_traits>
 
@@ -42,10 +42,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // every fragment offset stays linear in (ks, db).
 template <int D>
 constexpr int vrow_bytes() { return D * 2 + 32; }
-
-// max / sum of a value over the two lanes l and l ^ 32 (v_permlane32_swap).
-__device__ __forceinline__ float wave_max_halves(float x) { return fmaxf(x, wave_xor32(x)); }
-__device__ __forceinline__ float wave_sum_halves(float x) { return x + wave_xor32(x); }
 
 // D = 256 needs ~300 registers (O^T alone is 128) and 136 KB of LDS, one
 // workgroup per CU: it is built for one wave per SIMD.
@@ -116,6 +112,9 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[i][r] = 0.f;
   float m_i = -INFINITY;
+  // Row sum of the rounded fp16 P, in f32 adds: v_dot2_f32_f16 would add a
+  // pair per instruction but waits for the matrix core, which the other
+  // waves of the SIMD keep busy.
   float l_i = 0.f;
 
   u32x4 vreg[VPT];
@@ -238,7 +237,7 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
               mx4[(kb * 8 + r / 2) & 3], __builtin_elementwise_maximum(sacc[kb][r], sacc[kb][r + 1]));
       float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx4[0], mx4[1]),
                                                __builtin_elementwise_maximum(mx4[2], mx4[3]));
-      mx = __builtin_elementwise_maximum(mx, wave_xor32(mx)) * c2;
+      mx = half_max(mx) * c2;
 
       // Lazy rescaling: the reference max moves only when a row's max grows
       // by more than 2^8 (P then stays <= 256, exact range for fp16).
@@ -256,7 +255,6 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
       const float base = (m_i == -INFINITY) ? 0.f : m_i;
 
       // ---- P (fp16) per 16-key step, then O^T += V^T . P^T ----
-      const f16x2 ones = {(f16)1.0f, (f16)1.0f};
       const char* vptr = sV + vbase_off;
 #pragma unroll
       for (int ks = 0; ks < BN / 16; ++ks) {
@@ -270,7 +268,7 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
           f16x2 pair = __builtin_convertvector(pr, f16x2);
           pk[e] = pair[0];
           pk[e + 1] = pair[1];
-          l_i = __builtin_amdgcn_fdot2(pair, ones, l_i, false);
+          l_i += (float)pair[0] + (float)pair[1];
         }
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
@@ -298,7 +296,7 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
   }
 
   if (!active || qrow >= T) return;
-  const float l_tot = wave_sum_halves(l_i);
+  const float l_tot = half_sum(l_i);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   char* orow = p.o + ((int64_t)(seg + qrow) * p.o_stride + (int64_t)head * D) * (p.out_bf16 ? 2 : 4);
 #pragma unroll
@@ -329,7 +327,6 @@ constexpr int fast_lds() { return 2 * (BN * D * 2 + BN * vrow_bytes<D>()); }
 bool bf16_fast_kernel(int d, AttnKernelFn* fn, int* bn, int* nw, int* lds) {
   switch (d) {
     case 64: *fn = attn_bf16_kernel<64, 64, 4>; *bn = 64; *nw = 4; *lds = fast_lds<64, 64>(); return true;
-    case 128: *fn = attn_bf16_kernel<128, 64, 4>; *bn = 64; *nw = 4; *lds = fast_lds<128, 64>(); return true;
     case 256: *fn = attn_bf16_kernel<256, 64, 4>; *bn = 64; *nw = 4; *lds = fast_lds<256, 64>(); return true;
     default: return false;
   }

@@ -26,8 +26,25 @@ struct AttnParams {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ float wave_xor32(float x) {
-  return __shfl_xor(x, 32, 64);
+// Max / sum of x over lanes l and l ^ 32, without an LDS round trip:
+// v_permlane32_swap exchanges one half of the first register with the other
+// half of the second, so with both holding x, lane l sees x[l] in one and
+// x[l ^ 32] in the other (max and sum do not need to know which).
+__device__ __forceinline__ void swap_halves(float x, float* a, float* b) {
+  float u = x, v = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(v));
+  *a = u;
+  *b = v;
+}
+__device__ __forceinline__ float half_max(float x) {
+  float a, b;
+  swap_halves(x, &a, &b);
+  return __builtin_elementwise_maximum(a, b);
+}
+__device__ __forceinline__ float half_sum(float x) {
+  float a, b;
+  swap_halves(x, &a, &b);
+  return a + b;
 }
 
 // Byte offset of 16-byte chunk `c` of row `r` in a row-major tile whose rows
