@@ -40,8 +40,10 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <new>
+#include <queue>
 #include <vector>
 
 #include "attn_kernels.hpp"
@@ -421,6 +423,7 @@ struct KernelCfg {
   int nw;       // waves per workgroup
   int lds;      // dynamic LDS bytes
   int rows;     // query rows per wave (32 or 64)
+  bool persistent = false;  // one workgroup per CU over a host-assigned unit list
 };
 
 template <typename E, int D, int BN, int NW, bool PV16>
@@ -435,7 +438,11 @@ int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, bool fits32, K
   if (dtype == INL_BF16 && pv16 && fits32) {
     AttnKernelFn fn;
     int bn, nw, lds;
-    if (bf16_pp_kernel(head_dim, &fn, &bn, &nw, &lds) || bf16_fast_kernel(head_dim, &fn, &bn, &nw, &lds)) {
+    if (bf16_pp_kernel(head_dim, &fn, &bn, &nw, &lds)) {
+      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true};
+      return INL_OK;
+    }
+    if (bf16_fast_kernel(head_dim, &fn, &bn, &nw, &lds)) {
       *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32};
       return INL_OK;
     }
@@ -513,12 +520,91 @@ int validate_desc(const inl_attn_desc* d, int64_t* total_tokens) {
   return INL_OK;
 }
 
+size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
+
 struct Schedule {
+  // Work items (text, block of query rows, key-tile range), longest first.
+  // For a persistent kernel: work units (item, head group) in workgroup order.
   std::vector<int4> items;
+  std::vector<int32_t> unit_hg;   // persistent: head group of each unit
+  std::vector<int32_t> wg_start;  // persistent: workgroup b runs units [wg_start[b], wg_start[b + 1])
   int block_m = 0;
   int hpw = 1;
+  int n_hg = 1;
   KernelCfg cfg{};
+
+  // Device copy, one buffer: items, unit_hg, wg_start (16-byte aligned parts).
+  size_t hg_offset() const { return items.size() * sizeof(int4); }
+  size_t wg_offset() const { return hg_offset() + align16(unit_hg.size() * sizeof(int32_t)); }
+  size_t bytes() const { return items.empty() ? 0 : align16(wg_offset() + wg_start.size() * sizeof(int32_t)); }
+  std::vector<char> pack() const {
+    std::vector<char> b(bytes(), 0);
+    if (b.empty()) return b;
+    memcpy(b.data(), items.data(), hg_offset());
+    if (!unit_hg.empty()) memcpy(b.data() + hg_offset(), unit_hg.data(), unit_hg.size() * sizeof(int32_t));
+    if (!wg_start.empty()) memcpy(b.data() + wg_offset(), wg_start.data(), wg_start.size() * sizeof(int32_t));
+    return b;
+  }
+  int64_t n_units() const { return cfg.persistent ? (int64_t)items.size() : (int64_t)items.size() * n_hg; }
+  int64_t grid() const { return cfg.persistent ? (int64_t)wg_start.size() - 1 : n_units(); }
 };
+
+int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  return n;
+}
+
+struct CostedItem {
+  int4 it;
+  int cost;  // key tiles
+};
+
+// Persistent schedule: every (item, head group) unit goes to the workgroup
+// with the least work so far (longest units first, LPT). A workgroup costs
+// its tiles plus about one tile of per-unit overhead (Q load, output store).
+// Workgroups are dispatched to the 8 XCDs round-robin (b % 8), and each XCD
+// has its own L2; when the head groups split evenly over the XCDs, units of
+// head group h run only on workgroups b with b % 8 == h % 8, so the K/V rows
+// a head group reads are fetched into one L2.
+void assign_units(const std::vector<CostedItem>& items, int n_hg, Schedule* s) {
+  const int64_t U = (int64_t)items.size() * n_hg;
+  s->items.clear();
+  s->unit_hg.clear();
+  s->wg_start.assign(1, 0);
+  if (U == 0) return;
+  const int n_cu = device_cus();
+  const bool affinity = n_hg % 8 == 0;
+  const int classes = affinity ? 8 : 1;
+  int64_t n_wg = std::min<int64_t>(n_cu, U);
+  n_wg = std::max<int64_t>(n_wg, (U + PP_MAX_UNITS - 1) / PP_MAX_UNITS);
+  n_wg = (n_wg + classes - 1) / classes * classes;
+  std::vector<std::vector<int64_t>> lists(n_wg);  // unit = item * n_hg + hg
+  typedef std::pair<int64_t, int64_t> Load;       // (cost so far, workgroup)
+  std::vector<std::priority_queue<Load, std::vector<Load>, std::greater<Load>>> heaps(classes);
+  for (int64_t b = 0; b < n_wg; ++b) heaps[b % classes].push(Load(0, b));
+  for (size_t i = 0; i < items.size(); ++i)
+    for (int hg = 0; hg < n_hg; ++hg) {
+      auto& h = heaps[hg % classes];
+      Load top = h.top();
+      h.pop();
+      lists[top.second].push_back((int64_t)i * n_hg + hg);
+      if ((int)lists[top.second].size() < PP_MAX_UNITS) h.push(Load(top.first + 4 * items[i].cost + 3, top.second));
+    }
+  s->items.reserve(U);
+  s->unit_hg.reserve(U);
+  for (int64_t b = 0; b < n_wg; ++b) {
+    for (int64_t u : lists[b]) {
+      s->items.push_back(items[u / n_hg].it);
+      s->unit_hg.push_back((int32_t)(u % n_hg));
+    }
+    s->wg_start.push_back((int32_t)s->items.size());
+  }
+}
 
 int build_schedule(const inl_attn_desc* d, Schedule* s) {
   int64_t max_t = 0;
@@ -534,10 +620,10 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
   if (rc) return rc;
   const int group = d->h_q / d->h_kv;
   s->hpw = heads_per_wg(group, s->cfg.nw);
+  s->n_hg = d->h_kv * (group / s->hpw);
   s->block_m = s->cfg.rows * (s->cfg.nw / s->hpw);
   const int BM = s->block_m, BN = s->cfg.bn;
-  struct Tmp { int4 it; int cost; };
-  std::vector<Tmp> tmp;
+  std::vector<CostedItem> tmp;
   for (int b = 0; b < d->n_texts; ++b) {
     const int seg = d->seq_starts_host ? d->seq_starts_host[b] : d->cu_seqlens_host[b];
     const int T = d->cu_seqlens_host[b + 1] - d->cu_seqlens_host[b];
@@ -552,13 +638,21 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
       tmp.push_back({make_int4(seg, T, q0, (lo_t << 16) | hi_t), hi_t - lo_t});
     }
   }
-  std::stable_sort(tmp.begin(), tmp.end(), [](const Tmp& a, const Tmp& b) { return a.cost > b.cost; });
+  std::stable_sort(tmp.begin(), tmp.end(),
+                   [](const CostedItem& a, const CostedItem& b) { return a.cost > b.cost; });
+  if (s->cfg.persistent) {
+    if ((int64_t)tmp.size() * s->n_hg > INT32_MAX)
+      return fail(INL_E_UNSUPPORTED, "attention: too many tiles for one launch");
+    assign_units(tmp, s->n_hg, s);
+    return INL_OK;
+  }
   s->items.resize(tmp.size());
   for (size_t i = 0; i < tmp.size(); ++i) s->items[i] = tmp[i].it;
   return INL_OK;
 }
 
-AttnParams make_params(const inl_attn_desc* d, const Schedule& s, const int4* items,
+// `dev_sched`: the device copy of s.pack().
+AttnParams make_params(const inl_attn_desc* d, const Schedule& s, const void* dev_sched,
                        const void* q, const void* k, const void* v, void* out) {
   AttnParams p{};
   p.q = (const char*)q;
@@ -569,11 +663,13 @@ AttnParams make_params(const inl_attn_desc* d, const Schedule& s, const int4* it
   p.k_stride = d->k_row_stride ? d->k_row_stride : (int64_t)d->h_kv * d->head_dim;
   p.v_stride = d->v_row_stride ? d->v_row_stride : (int64_t)d->h_kv * d->head_dim;
   p.o_stride = d->o_row_stride ? d->o_row_stride : (int64_t)d->h_q * d->head_dim;
-  p.items = items;
+  p.items = (const int4*)dev_sched;
+  p.unit_hg = (const int32_t*)((const char*)dev_sched + s.hg_offset());
+  p.wg_start = (const int32_t*)((const char*)dev_sched + s.wg_offset());
   p.group = d->h_q / d->h_kv;
   p.hpw = s.hpw;
   p.groups_per_kv = p.group / s.hpw;
-  p.n_hg = d->h_kv * p.groups_per_kv;
+  p.n_hg = s.n_hg;
   p.rb = s.cfg.nw / s.hpw;
   p.head_dim = d->head_dim;
   p.causal = d->causal;
@@ -585,9 +681,10 @@ AttnParams make_params(const inl_attn_desc* d, const Schedule& s, const int4* it
 
 std::mutex g_attr_mu;
 
-int launch(const KernelCfg& cfg, const AttnParams& p, int64_t n_items, hipStream_t stream) {
-  if (n_items == 0) return INL_OK;
-  const int64_t blocks = n_items * p.n_hg;
+int launch(const Schedule& s, const AttnParams& p, hipStream_t stream) {
+  const KernelCfg& cfg = s.cfg;
+  const int64_t blocks = s.grid();
+  if (blocks <= 0) return INL_OK;
   if (blocks > 0x7fffffff) return fail(INL_E_UNSUPPORTED, "attention: too many tiles for one launch");
   {
     std::lock_guard<std::mutex> lock(g_attr_mu);
@@ -614,8 +711,8 @@ int check_ptrs(const void* q, const void* k, const void* v, const void* out, int
 
 struct inl_attn_plan {
   inl_attn_desc desc;     // cu_seqlens_host and seq_starts_host are not kept
-  inl::Schedule sched;    // items also kept on the host for inspection
-  int4* d_items = nullptr;
+  inl::Schedule sched;    // also kept on the host for inspection
+  void* d_sched = nullptr;
   int64_t total_tokens = 0;
 };
 
@@ -634,12 +731,12 @@ extern "C" int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** p
   pl->total_tokens = total;
   rc = build_schedule(desc, &pl->sched);
   if (rc) { delete pl; return rc; }
-  if (!pl->sched.items.empty()) {
-    const size_t bytes = pl->sched.items.size() * sizeof(int4);
-    hipError_t e = hipMalloc((void**)&pl->d_items, bytes);
+  const std::vector<char> blob = pl->sched.pack();
+  if (!blob.empty()) {
+    hipError_t e = hipMalloc(&pl->d_sched, blob.size());
     if (e != hipSuccess) { delete pl; return hip_fail(e, "hipMalloc(plan)"); }
-    e = hipMemcpy(pl->d_items, pl->sched.items.data(), bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) { (void)hipFree(pl->d_items); delete pl; return hip_fail(e, "hipMemcpy(plan)"); }
+    e = hipMemcpy(pl->d_sched, blob.data(), blob.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) { (void)hipFree(pl->d_sched); delete pl; return hip_fail(e, "hipMemcpy(plan)"); }
   }
   *plan = pl;
   return INL_OK;
@@ -648,8 +745,8 @@ extern "C" int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** p
 extern "C" int inl_attn_plan_destroy(inl_attn_plan* plan) {
   if (!plan) return INL_OK;
   int rc = INL_OK;
-  if (plan->d_items) {
-    hipError_t e = hipFree(plan->d_items);
+  if (plan->d_sched) {
+    hipError_t e = hipFree(plan->d_sched);
     if (e != hipSuccess) rc = inl::hip_fail(e, "hipFree(plan)");
   }
   delete plan;
@@ -659,7 +756,7 @@ extern "C" int inl_attn_plan_destroy(inl_attn_plan* plan) {
 extern "C" int inl_attn_plan_info(const inl_attn_plan* plan, int64_t* n_tiles,
                                   int32_t* block_m, int32_t* block_n) {
   if (!plan) return inl::fail(INL_E_INVALID, "attention: plan is NULL");
-  if (n_tiles) *n_tiles = (int64_t)plan->sched.items.size() * (plan->desc.h_q / plan->sched.hpw);
+  if (n_tiles) *n_tiles = plan->sched.n_units();
   if (block_m) *block_m = plan->sched.block_m;
   if (block_n) *block_n = plan->sched.cfg.bn;
   return INL_OK;
@@ -671,8 +768,8 @@ extern "C" int inl_attn_fwd(const inl_attn_plan* plan, const void* q, const void
   if (!plan) return fail(INL_E_INVALID, "attention: plan is NULL");
   int rc = check_ptrs(q, k, v, out, plan->total_tokens);
   if (rc) return rc;
-  AttnParams p = make_params(&plan->desc, plan->sched, plan->d_items, q, k, v, out);
-  return launch(plan->sched.cfg, p, (int64_t)plan->sched.items.size(), (hipStream_t)stream);
+  AttnParams p = make_params(&plan->desc, plan->sched, plan->d_sched, q, k, v, out);
+  return launch(plan->sched, p, (hipStream_t)stream);
 }
 
 extern "C" int inl_attn_workspace_size(const inl_attn_desc* desc, size_t* bytes) {
@@ -684,7 +781,7 @@ extern "C" int inl_attn_workspace_size(const inl_attn_desc* desc, size_t* bytes)
   Schedule s;
   rc = build_schedule(desc, &s);
   if (rc) return rc;
-  *bytes = s.items.size() * sizeof(int4);
+  *bytes = s.bytes();
   return INL_OK;
 }
 
@@ -700,13 +797,14 @@ extern "C" int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q, con
   Schedule s;
   rc = build_schedule(desc, &s);
   if (rc) return rc;
-  const size_t need = s.items.size() * sizeof(int4);
+  const size_t need = s.bytes();
   if (need == 0) return INL_OK;
   if (!workspace || workspace_bytes < need)
     return fail(INL_E_INVALID, "attention: workspace is NULL or smaller than inl_attn_workspace_size()");
   if (!aligned16(workspace)) return fail(INL_E_INVALID, "attention: workspace must be 16-byte aligned");
-  rc = upload_async(workspace, s.items.data(), need, (hipStream_t)stream);
+  const std::vector<char> blob = s.pack();
+  rc = upload_async(workspace, blob.data(), need, (hipStream_t)stream);
   if (rc) return rc;
-  AttnParams p = make_params(desc, s, (const int4*)workspace, q, k, v, out);
-  return launch(s.cfg, p, (int64_t)s.items.size(), (hipStream_t)stream);
+  AttnParams p = make_params(desc, s, workspace, q, k, v, out);
+  return launch(s, p, (hipStream_t)stream);
 }

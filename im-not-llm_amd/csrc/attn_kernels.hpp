@@ -12,7 +12,12 @@ struct AttnParams {
   char* o;
   int64_t q_stride, k_stride, v_stride, o_stride;  // elements between token rows
   const int4* items;  // {seg_start, seg_len, q0, (lo_tile << 16) | hi_tile}
-  int32_t n_hg;       // workgroups per item
+  // Persistent kernels only: items[] holds work units (item, head group),
+  // unit_hg[u] the head group of unit u, and workgroup b runs units
+  // wg_start[b] .. wg_start[b + 1] - 1 in order.
+  const int32_t* unit_hg;
+  const int32_t* wg_start;
+  int32_t n_hg;       // head groups per item (workgroups per item unless persistent)
   int32_t groups_per_kv;  // (h_q / h_kv) / hpw
   int32_t group;      // h_q / h_kv
   int32_t hpw;        // query heads per workgroup
@@ -60,7 +65,9 @@ typedef void (*AttnKernelFn)(AttnParams);
 bool bf16_fast_kernel(int head_dim_padded, AttnKernelFn* fn, int* bn, int* nw, int* lds);
 
 // Ping-pong bf16 kernel (attn_pp.hip): 8 waves in two groups that alternate
-// MFMA and softmax phases; head dim 128.
+// MFMA and softmax phases; head dim 128. Persistent: one workgroup per CU,
+// each running a host-assigned list of at most PP_MAX_UNITS work units.
+constexpr int PP_MAX_UNITS = 1024;
 bool bf16_pp_kernel(int head_dim, AttnKernelFn* fn, int* bn, int* nw, int* lds);
 
 }  // namespace inl

@@ -88,12 +88,14 @@ __device__ __forceinline__ void lds_barrier() {
 
 template <int D, int BN>
 struct PPShape {
+  static_assert(PP_MAX_UNITS % 4 == 0, "descriptor table alignment");
   static constexpr int NT = 512;            // 8 waves
   static constexpr int CH = D / 8;          // 16-byte chunks per row
   static constexpr int ROW = D * 2;         // bytes per K or V row in LDS
   static constexpr int TILE = BN * ROW;     // bytes per stage
   static constexpr int STAGES = 4;
-  static constexpr int LDS = 2 * STAGES * TILE;
+  static constexpr int TILES_LDS = 2 * STAGES * TILE;
+  static constexpr int LDS = TILES_LDS + PP_MAX_UNITS * (16 + 4);
   static constexpr int KPW = TILE / 1024 / 8;  // 1 KB direct loads per wave per tile (K and V each)
   static constexpr int RPB = 1024 / ROW;       // rows per 1 KB block
   static_assert(D == 128, "swizzles are laid out for 16 chunks per row");
@@ -120,35 +122,40 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   const int lq = lane & 31;
   const int hf = lane >> 5;
 
-  const int item_idx = blockIdx.x / p.n_hg;
-  const int hg = blockIdx.x - item_idx * p.n_hg;
-  const int4 it = p.items[item_idx];
-  const int seg = it.x;
-  const int T = it.y;
-  const int q0 = it.z;
-  const int lo_t = it.w >> 16;
-  const int hi_t = it.w & 0xffff;
-  const int kvh = hg / p.groups_per_kv;
-  const int head = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + wave / p.rb;
-  const int r0 = q0 + (wave % p.rb) * 32;
-  const bool active = r0 < T;
+  // ---- this workgroup's work units (host-ordered), staged in LDS ----
+  const int u_first = p.wg_start[blockIdx.x];
+  const int nu = p.wg_start[blockIdx.x + 1] - u_first;
+  if (nu <= 0) return;
+  int4* const sdesc = reinterpret_cast<int4*>(smem + S::TILES_LDS);
+  int* const shg = reinterpret_cast<int*>(sdesc + PP_MAX_UNITS);
+  for (int i = tid; i < nu; i += S::NT) {
+    sdesc[i] = p.items[u_first + i];
+    shg[i] = p.unit_hg[u_first + i];
+  }
+  // The stream's first PV product reads V stage 3 with P = 0: zero it, so
+  // that no stale LDS bits (NaN as fp16) reach the accumulator.
+  for (int i = tid; i < S::TILE / 16; i += S::NT)
+    reinterpret_cast<u32x4*>(sVb + (S::STAGES - 1) * S::TILE)[i] = (u32x4){0u, 0u, 0u, 0u};
+  __syncthreads();
+
   const int causal = p.causal;
   const int window = p.window;
-
-  const int rlast = min(r0 + 31, T - 1);
-  int klo = 0, khi = causal ? min(T, r0 + 32) : T;
-  if (window >= 0) {
-    klo = max(0, r0 - window);
-    khi = min(khi, rlast + window + 1);
-  }
-
   const uint32_t kst_b = (uint32_t)(p.k_stride * 2);
   const uint32_t vst_b = (uint32_t)(p.v_stride * 2);
   const uint32_t qst_b = (uint32_t)(p.q_stride * 2);
-  const i32x4 krs = pp_rsrc_words(p.k + ((int64_t)seg * p.k_stride + (int64_t)kvh * D) * 2, (uint32_t)T * kst_b);
-  const i32x4 vrs = pp_rsrc_words(p.v + ((int64_t)seg * p.v_stride + (int64_t)kvh * D) * 2, (uint32_t)T * vst_b);
-  const __amdgpu_buffer_rsrc_t qrs =
-      pp_rsrc(p.q + ((int64_t)seg * p.q_stride + (int64_t)head * D) * 2, (uint32_t)T * qst_b);
+  const int osz = p.out_bf16 ? 2 : 4;
+
+  // Unit u: {text start row, text length, first query row, lo_tile << 16 | hi_tile}
+  // and its head group; read wave-uniformly from LDS.
+  auto unit = [&](int u, int& seg, int& T, int& q0, int& lo, int& hi, int& hg) __attribute__((always_inline)) {
+    const int4 d = sdesc[u];
+    seg = __builtin_amdgcn_readfirstlane(d.x);
+    T = __builtin_amdgcn_readfirstlane(d.y);
+    q0 = __builtin_amdgcn_readfirstlane(d.z);
+    lo = __builtin_amdgcn_readfirstlane(d.w) >> 16;
+    hi = __builtin_amdgcn_readfirstlane(d.w) & 0xffff;
+    hg = __builtin_amdgcn_readfirstlane(shg[u]);
+  };
 
   // ---- per-lane constant offsets ----
   // This wave's slice of every tile: 1 KB blocks i * 8 + wave. Lane l of a
@@ -181,32 +188,94 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   for (int db = 0; db < NDB; ++db)
     voff[db] = vrow * S::ROW + ((((4 * db + (vcol >> 3)) ^ ((vrow & 3) << 2)) << 4) | ((vcol * 2) & 15));
 
-  // ---- loads ----
-  auto stage_of = [&](int t) __attribute__((always_inline)) { return (uint32_t)((t - lo_t) & (S::STAGES - 1)); };
-  auto issue_tile = [&](int t) __attribute__((always_inline)) {
-    const uint32_t st = stage_of(t) * S::TILE;
-    const uint32_t kbase = (uint32_t)(t * BN) * kst_b;
-    const uint32_t vbase = (uint32_t)(t * BN) * vst_b;
+  // ---- load cursor: the next tile of this workgroup's tile stream to load ----
+  // Every wave loads its slice of every stream tile, in stream order, into
+  // stage (stream index) % 4. Past the stream's end the descriptors get an
+  // empty range: the loads still go out (the loop has no branch for them)
+  // and return zeros into a stage that no later phase reads.
+  int du = 0, dt = 0, dhi = 0;
+  i32x4 krs, vrs;
+  auto dma_unit = [&](int u) __attribute__((always_inline)) {
+    if (u < nu) {
+      int seg, T, q0, lo, hi, hg;
+      unit(u, seg, T, q0, lo, hi, hg);
+      const int kvh = hg / p.groups_per_kv;
+      krs = pp_rsrc_words(p.k + ((int64_t)seg * p.k_stride + (int64_t)kvh * D) * 2, (uint32_t)T * kst_b);
+      vrs = pp_rsrc_words(p.v + ((int64_t)seg * p.v_stride + (int64_t)kvh * D) * 2, (uint32_t)T * vst_b);
+      dt = lo;
+      dhi = hi;
+    } else {
+      krs[2] = 0;
+      vrs[2] = 0;
+      dhi = 0x7fffffff;
+    }
+  };
+  // Part i of the cursor's tile (K blocks, then V blocks) into the stage at
+  // byte offset `st`. The parts are spread over a softmax phase: a CU's
+  // address units take a while to accept a group's 16 loads, and a wave that
+  // issues its loads back to back stalls until they are accepted.
+  constexpr int DMA_PARTS = 2 * S::KPW;
+  const uint32_t dma_lds = lds0 + wave * 1024;
+  auto dma_part = [&](int i, uint32_t st) __attribute__((always_inline)) {
+    if (i < S::KPW)
+      dma_b128(krs, dma_lds + st + i * 8192, (uint32_t)(dt * BN) * kst_b + kg_off[i]);
+    else
+      dma_b128(vrs, dma_lds + S::STAGES * S::TILE + st + (i - S::KPW) * 8192,
+               (uint32_t)(dt * BN) * vst_b + vg_off[i - S::KPW]);
+  };
+  auto dma_advance = [&]() __attribute__((always_inline)) {
+    if (__builtin_expect(++dt == dhi, 0)) dma_unit(++du);
+  };
+  auto dma_tile = [&](uint32_t st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < S::KPW; ++i)
-      dma_b128(krs, lds0 + st + (i * 8 + wave) * 1024, kbase + kg_off[i]);
-#pragma unroll
-    for (int i = 0; i < S::KPW; ++i)
-      dma_b128(vrs, lds0 + S::STAGES * S::TILE + st + (i * 8 + wave) * 1024, vbase + vg_off[i]);
+    for (int i = 0; i < DMA_PARTS; ++i) dma_part(i, st);
+    dma_advance();
   };
 
-  // ---- prologue: tile lo in flight, Q^T operand into registers ----
-  // Q rows past the text load as zero. The compiler-visible wait for the Q
-  // loads also retires tile lo's loads; after it the compiler tracks no
-  // outstanding global loads, so it never inserts waits of its own later.
-  const int qrow = r0 + lq;
+  // ---- compute cursor: the unit whose tiles this wave's phases process ----
+  int cu = 0;
+  int seg = 0, T = 0, lo_t = 0, hi_t = 0, r0 = 0, rlast = 0, head = 0;
+  int f_lo = 0, f_n = 0;     // tiles f_lo .. f_lo + f_n - 1 need no mask for this wave's rows
+  bool active = false;
+  __amdgpu_buffer_rsrc_t qrs;
+  auto set_unit = [&](int u) __attribute__((always_inline)) {
+    int q0, hg;
+    unit(u, seg, T, q0, lo_t, hi_t, hg);
+    const int kvh = hg / p.groups_per_kv;
+    head = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + wave / p.rb;
+    r0 = q0 + (wave % p.rb) * 32;
+    active = r0 < T;
+    rlast = min(r0 + 31, T - 1);
+    // Tile j needs no mask iff j * BN + BN <= e and j * BN >= b (see
+    // apply_mask): e bounds the text, the causal diagonal of the first row
+    // and the window of the first row, b the window of the last row.
+    int e = T;
+    if (causal) e = min(e, r0 + 1);
+    if (window >= 0) e = min(e, r0 + window + 1);
+    const int f_hi = active ? e / BN : 0;
+    f_lo = window >= 0 ? (max(0, rlast - window) + BN - 1) / BN : 0;
+    f_n = max(0, f_hi - f_lo);
+    qrs = pp_rsrc(p.q + ((int64_t)seg * p.q_stride + (int64_t)head * D) * 2, (uint32_t)T * qst_b);
+  };
   u32x4 qreg[KST];
-  if (lo_t < hi_t) issue_tile(lo_t);
+  // Q^T operand of the current unit (rows past the text load as zero).
+  auto load_q = [&]() __attribute__((always_inline)) {
+    const uint32_t qrow_b = (uint32_t)(r0 + lq) * qst_b;
 #pragma unroll
-  for (int i = 0; i < KST; ++i)
-    qreg[i] = __builtin_amdgcn_raw_buffer_load_b128(qrs, (uint32_t)qrow * qst_b + (2 * i + hf) * 16, 0, 0);
+    for (int i = 0; i < KST; ++i)
+      qreg[i] = __builtin_amdgcn_raw_buffer_load_b128(qrs, qrow_b + (2 * i + hf) * 16, 0, 0);
+  };
+
+  // ---- prologue: stream tiles 0 and 1 in flight, unit 0's Q ----
+  // The compiler-visible wait for the Q loads also retires tile 0's loads;
+  // after it the compiler tracks no outstanding global loads, so it inserts
+  // no waits of its own into the loop.
+  dma_unit(0);
+  set_unit(0);
+  dma_tile(0);
+  load_q();
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  if (lo_t + 1 < hi_t) issue_tile(lo_t + 1);
+  dma_tile(S::TILE);
   lds_barrier();
 
   f32x16 oacc[NDB];
@@ -220,19 +289,15 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   // of the SIMD keeps busy.
   float l_i = 0.f;
   f32x16 sacc[NKB];
-  u32x4 pk[PKS];   // P^T operand per PV k-step: four packed fp16 pairs
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+  // P^T operand per PV k-step (four packed fp16 pairs); zero for the first
+  // step's PV, which reads the zeroed stage 3.
+  u32x4 pk[PKS];
 #pragma unroll
   for (int ks = 0; ks < PKS; ++ks)
 #pragma unroll
     for (int e = 0; e < 4; ++e) pk[ks][e] = 0u;
 
   const float c2 = p.scale_log2;
-
-  auto tile_on = [&](int t) __attribute__((always_inline)) { return active && t * BN < khi && t * BN + BN > klo; };
 
   // LDS fragments are read two MFMA groups ahead of their use (V^T in two
   // register sets, K in a ring of three); sched_barriers keep the compiler
@@ -248,12 +313,14 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       dst[db] = (f16x8){h1[0], h1[1], h1[2], h1[3], h2[0], h2[1], h2[2], h2[3]};
     }
   };
-  auto kfrag = [&](const char* sK, int st, bf16x8* dst) __attribute__((always_inline)) {
+  // (u32x4 rather than bf16x8: register copies of bf16 vectors are split
+  // into 16-bit halves and repacked.)
+  auto kfrag = [&](const char* sK, int st, u32x4* dst) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) dst[kb] = *reinterpret_cast<const bf16x8*>(sK + kb * 32 * S::ROW + koff[st]);
+    for (int kb = 0; kb < NKB; ++kb) dst[kb] = *reinterpret_cast<const u32x4*>(sK + kb * 32 * S::ROW + koff[st]);
   };
   // S^T = K Q^T with kr[0], kr[1] already holding the fragments of steps 0, 1.
-  auto qk_body = [&](const char* sK, bf16x8 (*kr)[NKB]) __attribute__((always_inline)) {
+  auto qk_body = [&](const char* sK, u32x4 (*kr)[NKB]) __attribute__((always_inline)) {
     const f32x16 zero = {};
 #pragma unroll
     for (int st = 0; st < KST; ++st) {
@@ -261,7 +328,8 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[st % 3][kb], __builtin_bit_cast(bf16x8, qreg[st]),
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[st % 3][kb]),
+                                                           __builtin_bit_cast(bf16x8, qreg[st]),
                                                            st == 0 ? zero : sacc[kb], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -285,53 +353,100 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     }
   };
 
-  // ---- MFMA phase of tile j ----
-  // Fragment reads for the first MFMAs go out first, then the reads of the V
-  // slice to convert; the conversion itself sits between PV k-steps.
-  auto mphase = [&](int j) __attribute__((always_inline)) {
-    const bool do_pv = j > lo_t && tile_on(j - 1);
-    const bool do_qk = j < hi_t && tile_on(j);
-    const bool do_cv = j < hi_t;
-    const char* sK = sKb + stage_of(j) * S::TILE;
-    char* sVc = sVb + stage_of(j) * S::TILE;
-    u32x4 w[S::KPW];
-    bf16x8 kr[3][NKB];
-    if (do_pv) {
-      const char* sV = sVb + stage_of(j - 1) * S::TILE;
-      f16x8 vs[2][NDB];
-      vfrag(sV, 0, vs[0]);
-      vfrag(sV, 1, vs[1]);
-      if (do_cv) conv_read(sVc, w);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int ks = 0; ks < PKS; ++ks) {
+  // Output of the unit whose O^T is accumulating: o_row points at this
+  // lane's first output column (4 * hf) of its query row, so the columns a
+  // lane stores are o_row + compile-time offsets. Captured when the compute
+  // cursor leaves the unit; stored after the unit's last PV.
+  char* o_row = nullptr;
+  bool o_valid = false;
+  auto capture_out = [&]() __attribute__((always_inline)) {
+    const int qrow = r0 + lq;
+    o_valid = active && qrow < T;
+    o_row = p.o + ((int64_t)(seg + (o_valid ? qrow : 0)) * p.o_stride + (int64_t)head * D + 4 * hf) * osz;
+  };
+  auto store_out = [&]() __attribute__((always_inline)) {
+    const float l_tot = half_sum(l_i);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (o_valid) {
+      if (p.out_bf16) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vs[ks & 1][db], __builtin_bit_cast(f16x8, pk[ks]),
-                                                            oacc[db], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (ks + 2 < PKS) vfrag(sV, ks + 2, vs[ks & 1]);
-        if (ks + 2 >= PKS && do_qk) kfrag(sK, ks + 2 - PKS, kr[ks + 2 - PKS]);
-        __builtin_amdgcn_sched_barrier(0);
-        if (ks == 1 && do_cv) conv_write(sVc, w);
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            bf16x4 val;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) val[e] = (bf16)(oacc[db][4 * g + e] * inv);
+            *reinterpret_cast<bf16x4*>(o_row + (db * 32 + 8 * g) * 2) = val;
+          }
+      } else {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            f32x4 val;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e] * inv;
+            *reinterpret_cast<f32x4*>(o_row + (db * 32 + 8 * g) * 4) = val;
+          }
       }
-    } else {
-      if (do_qk) {
-        kfrag(sK, 0, kr[0]);
-        kfrag(sK, 1, kr[1]);
-      }
-      if (do_cv) conv_read(sVc, w);
-      __builtin_amdgcn_sched_barrier(0);
-      if (do_cv) conv_write(sVc, w);
     }
+#pragma unroll
+    for (int i = 0; i < NDB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[i][r] = 0.f;
+    m_i = -INFINITY;
+    l_i = 0.f;
+  };
+
+  // ---- MFMA phase of the stream step whose K and V are in stage `st` ----
+  // O^T += V^T P^T of the previous step (stage st - 1), the store of a
+  // finished unit's output (fin), S^T = K Q^T of this step, and the
+  // conversion of this wave's slice of this step's V. Fragment reads for the
+  // first MFMAs go out first, then the reads of the V slice to convert; the
+  // conversion itself sits between PV k-steps. Every product is computed on
+  // every step: tiles (or rows) a wave does not see are masked to P = 0 by
+  // the softmax, which costs less than branching around them. LAST: the
+  // step after the stream's end, PV and store only.
+  bool fin = false;
+  auto mphase = [&](auto last_tag, uint32_t st) __attribute__((always_inline)) {
+    constexpr bool LAST = decltype(last_tag)::value;
+    const char* sK = sKb + st;
+    char* sVc = sVb + st;
+    const char* sV = sVb + ((st + (S::STAGES - 1) * S::TILE) & (S::STAGES * S::TILE - 1));
+    u32x4 w[S::KPW];
+    u32x4 kr[3][NKB];
+    f16x8 vs[2][NDB];
+    vfrag(sV, 0, vs[0]);
+    vfrag(sV, 1, vs[1]);
+    if (!LAST) conv_read(sVc, w);
     __builtin_amdgcn_sched_barrier(0);
-    if (do_qk) qk_body(sK, kr);
+#pragma unroll
+    for (int ks = 0; ks < PKS; ++ks) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vs[ks & 1][db], __builtin_bit_cast(f16x8, pk[ks]),
+                                                          oacc[db], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 2 < PKS) vfrag(sV, ks + 2, vs[ks & 1]);
+      if (!LAST && ks + 2 >= PKS) kfrag(sK, ks + 2 - PKS, kr[ks + 2 - PKS]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (!LAST && ks == 1) conv_write(sVc, w);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (__builtin_expect(fin, 0)) {
+      store_out();
+      fin = false;
+    }
+    if (!LAST) qk_body(sK, kr);
   };
 
   // P (fp16) and its per-lane sum over this tile, with reference max `base`.
-  auto make_p = [&](float base) __attribute__((always_inline)) {
-    float lt = 0.f;
+  // The sum adds the rounded fp16 values with v_fma_mix_f32 (f16 operand,
+  // times 1, plus f32: one instruction per value; the compiler would emit a
+  // conversion and an add). `after_step(ks)` runs after each PV k-step's
+  // worth of P.
+  auto make_p = [&](float base, auto&& after_step) __attribute__((always_inline)) {
+    float lt0 = 0.f, lt1 = 0.f;
 #pragma unroll
     for (int ks = 0; ks < PKS; ++ks) {
 #pragma unroll
@@ -340,12 +455,14 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
         const float x1 = sacc[ks >> 1][8 * (ks & 1) + e + 1];
         f32x2 pr = {__builtin_amdgcn_exp2f(__builtin_fmaf(x0, c2, -base)),
                     __builtin_amdgcn_exp2f(__builtin_fmaf(x1, c2, -base))};
-        f16x2 pair = __builtin_convertvector(pr, f16x2);
-        pk[ks][e / 2] = __builtin_bit_cast(uint32_t, pair);
-        lt += (float)pair[0] + (float)pair[1];
+        const uint32_t pair = __builtin_bit_cast(uint32_t, __builtin_convertvector(pr, f16x2));
+        pk[ks][e / 2] = pair;
+        asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(lt0) : "v"(pair));
+        asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lt1) : "v"(pair));
       }
+      after_step(ks);
     }
-    return lt;
+    return lt0 + lt1;
   };
   auto apply_mask = [&](int j) __attribute__((always_inline)) {
     const int kt0 = j * BN;
@@ -366,13 +483,20 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       }
   };
 
-  // ---- softmax of tile j (S^T in sacc) ----
-  auto softmax = [&](int j) __attribute__((always_inline)) {
-    const int kt0 = j * BN;
-    const bool need_mask =
-        (kt0 + BN > T) || (causal && kt0 + BN - 1 > r0) ||
-        (window >= 0 && (rlast - kt0 > window || kt0 + BN - 1 - r0 > window));
-    if (need_mask) apply_mask(j);
+  // ---- softmax phase of tile t of the current unit (S^T in sacc) ----
+  // The next stream tile's loads go to the stage at byte offset `dst` (two
+  // tiles ahead of group 0's MFMA phases, three ahead of group 1's): one part
+  // before the row max (which waits for the last QK^T MFMAs), the others
+  // between P's k-steps. On the unit's last tile the next unit's Q is loaded
+  // too and the cursor moves on. At the end the wave waits for the loads it
+  // issued one phase earlier, which the next MFMA phases read (all of its
+  // loads, when it moved to a new unit). Returns false after the stream's
+  // last tile.
+  int t = lo_t;
+  auto vphase = [&](uint32_t dst) __attribute__((always_inline)) {
+    dma_part(0, dst);
+    __builtin_amdgcn_sched_barrier(0);
+    if (__builtin_expect((uint32_t)(t - f_lo) >= (uint32_t)f_n, 0)) apply_mask(t);
     // Row max (v_maximum3: no NaN canonicalisation), across the two halves.
     float mx4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
@@ -386,7 +510,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     mx = half_max(mx) * c2;
     // Lazy rescaling: the reference max moves only when a row's max grows by
     // more than 2^8 (P then stays <= 256, well inside fp16's range).
-    if (__builtin_amdgcn_ballot_w64(mx > m_i + 8.0f)) {
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(mx > m_i + 8.0f) != 0, 0)) {
       const float m_new = __builtin_elementwise_maximum(m_i, mx);
       // m_i == -inf: nothing accumulated yet (alpha 0, and no -inf - -inf).
       const float alpha = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_new);
@@ -397,62 +521,66 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
     }
-    l_i += make_p(m_i == -INFINITY ? 0.f : m_i);
-  };
-
-  // ---- softmax phase of tile j for this wave's group ----
-  // Loads of tile j + grp + 2 go out first; at the end the wave waits for the
-  // loads it issued one phase earlier (tile j + grp + 1), which the next MFMA
-  // phases read.
-  auto vphase = [&](int j) __attribute__((always_inline)) {
-    const int x = j + grp + 2;
-    const bool more = x < hi_t;
-    if (more) issue_tile(x);
+    l_i += make_p(m_i == -INFINITY ? 0.f : m_i, [&](int ks) __attribute__((always_inline)) {
+      if (ks + 1 < DMA_PARTS) {
+        __builtin_amdgcn_sched_barrier(0);
+        dma_part(ks + 1, dst);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    });
+#pragma unroll
+    for (int i = PKS + 1; i < DMA_PARTS; ++i) dma_part(i, dst);
     __builtin_amdgcn_sched_barrier(0);
-    if (j >= lo_t && j < hi_t && tile_on(j)) softmax(j);
-    if (more) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::KPW) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    dma_advance();
+    if (__builtin_expect(t + 1 == hi_t, 0)) {
+      capture_out();
+      fin = true;
+      if (cu + 1 < nu) {
+        set_unit(++cu);
+        t = lo_t;
+        load_q();
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        return true;
+      }
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::KPW) : "memory");
+      return false;
+    }
+    ++t;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::KPW) : "memory");
+    return true;
   };
 
-  // Half-slots, barrier-separated. Group 0: M(lo) V(lo) ... M(hi-1) V(hi-1)
-  // M(hi) [PV of the last tile] and one empty half-slot; group 1 starts one
-  // half-slot earlier with V(lo-1) (loads only) and ends with M(hi).
+  // ---- the stream, in barrier-separated half-slots ----
+  // Group 0: M(0) V(0) M(1) V(1) ... M(end) [PV and store of the last tile]
+  // and one empty half-slot; group 1 starts one half-slot earlier with a
+  // phase that only issues loads, and ends with M(end). The loop is unrolled
+  // over the 4 stages so that every LDS stage offset is an immediate.
+  auto step = [&](auto stage_tag) __attribute__((always_inline)) {
+    constexpr uint32_t SI = decltype(stage_tag)::value;
+    mphase(std::false_type{}, SI * S::TILE);
+    lds_barrier();
+    const uint32_t dst = grp ? ((SI + 3) & 3) * S::TILE : ((SI + 2) & 3) * S::TILE;
+    const bool more = vphase(dst);
+    lds_barrier();
+    return more;
+  };
   if (grp) {
-    vphase(lo_t - 1);
+    dma_tile(2 * S::TILE);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::KPW) : "memory");
     lds_barrier();
   }
-  for (int j = lo_t; j < hi_t; ++j) {
-    mphase(j);
-    lds_barrier();
-    vphase(j);
-    lds_barrier();
+  uint32_t end_st;
+  for (;;) {
+    if (!step(std::integral_constant<uint32_t, 0>{})) { end_st = 1; break; }
+    if (!step(std::integral_constant<uint32_t, 1>{})) { end_st = 2; break; }
+    if (!step(std::integral_constant<uint32_t, 2>{})) { end_st = 3; break; }
+    if (!step(std::integral_constant<uint32_t, 3>{})) { end_st = 0; break; }
   }
-  mphase(hi_t);
+  mphase(std::true_type{}, end_st * S::TILE);
+  // Loads past the stream's end may still be writing LDS.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   lds_barrier();
   if (!grp) lds_barrier();
-
-  if (!active || qrow >= T) return;
-  const float l_tot = half_sum(l_i);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  char* orow = p.o + ((int64_t)(seg + qrow) * p.o_stride + (int64_t)head * D) * (p.out_bf16 ? 2 : 4);
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = db * 32 + 8 * g + 4 * hf;
-      if (p.out_bf16) {
-        bf16x4 val;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) val[e] = (bf16)(oacc[db][4 * g + e] * inv);
-        *reinterpret_cast<bf16x4*>(orow + d0 * 2) = val;
-      } else {
-        f32x4 val;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e] * inv;
-        *reinterpret_cast<f32x4*>(orow + d0 * 4) = val;
-      }
-    }
-  }
 }
 
 }  // namespace
