@@ -135,7 +135,7 @@ def cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale, seconds):
 
 def read_traffic(name: str):
     """HBM bytes per launch from the committed PMC summary, if present."""
-    f = ROOT / "profiles" / f"attn_fwd_{name}_pmc.md"
+    f = ROOT / "profiles" / f"attn_pp_{name}_pmc.md"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
