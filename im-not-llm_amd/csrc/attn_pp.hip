@@ -75,6 +75,24 @@ __device__ __forceinline__ void dma_b128(i32x4 rsrc, uint32_t lds, uint32_t voff
                :: "v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 
+// LDS access at an integer byte address: with a per-lane base register and a
+// compile-time offset the offset lands in the instruction's offset field.
+template <typename T>
+__device__ __forceinline__ T lds_load(uint32_t a) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>((size_t)a);
+}
+template <typename T>
+__device__ __forceinline__ void lds_store(uint32_t a, const T& v) {
+  *reinterpret_cast<__attribute__((address_space(3))) T*>((size_t)a) = v;
+}
+
+// Hides a value's provenance from the optimizer, so that base + constant is
+// not reassociated into constant + base (which would cost an add per use).
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(size_t)PP_LDS_PTR(p));
 }
@@ -162,7 +180,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   // block fills LDS slot l: row blk * RPB + l / CH, physical chunk l % CH,
   // and so loads the logical chunk the swizzle puts there.
   uint32_t kg_off[S::KPW], vg_off[S::KPW];   // global byte offsets within a tile
-  int cv_off[S::KPW];                         // LDS byte offset of the V chunk this lane converts
+  uint32_t cv_a[S::KPW];                      // LDS address of the stage-0 V chunk this lane converts
 #pragma unroll
   for (int i = 0; i < S::KPW; ++i) {
     const int blk = i * 8 + wave;
@@ -170,12 +188,12 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     const int pc = lane % S::CH;
     kg_off[i] = (uint32_t)row * kst_b + ((pc ^ (row & 15)) << 4);
     vg_off[i] = (uint32_t)row * vst_b + ((pc ^ ((row & 3) << 2)) << 4);
-    cv_off[i] = blk * 1024 + lane * 16;
+    cv_a[i] = opaque(lds0 + S::STAGES * S::TILE + blk * 1024 + lane * 16);
   }
   // QK^T fragment of step st (rows lq, lq + 32): logical chunk 2 st + hf.
-  int koff[KST];
+  uint32_t ka[KST];   // LDS address of the fragment in stage 0
 #pragma unroll
-  for (int st = 0; st < KST; ++st) koff[st] = lq * S::ROW + (((2 * st + hf) ^ (lq & 15)) << 4);
+  for (int st = 0; st < KST; ++st) ka[st] = opaque(lds0 + lq * S::ROW + (((2 * st + hf) ^ (lq & 15)) << 4));
   // PV fragment (db, ks, half): rows ks*16 + 8*half + vrow, logical columns
   // db*32 + vcol .. +3. The swizzle of those rows depends on vrow & 3 only,
   // so each db has one per-lane base and ks / half are immediate offsets.
@@ -183,10 +201,11 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   const int j16 = lane & 15;
   const int vcol = 16 * (g16 & 1) + 4 * (j16 & 3);
   const int vrow = 4 * hf + (j16 >> 2);
-  int voff[NDB];
+  uint32_t va[NDB];   // LDS address of the fragment in stage 0
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
-    voff[db] = vrow * S::ROW + ((((4 * db + (vcol >> 3)) ^ ((vrow & 3) << 2)) << 4) | ((vcol * 2) & 15));
+    va[db] = opaque(lds0 + S::STAGES * S::TILE + vrow * S::ROW +
+                    ((((4 * db + (vcol >> 3)) ^ ((vrow & 3) << 2)) << 4) | ((vcol * 2) & 15)));
 
   // ---- load cursor: the next tile of this workgroup's tile stream to load ----
   // Every wave loads its slice of every stream tile, in stream order, into
@@ -265,6 +284,23 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     for (int i = 0; i < KST; ++i)
       qreg[i] = __builtin_amdgcn_raw_buffer_load_b128(qrs, qrow_b + (2 * i + hf) * 16, 0, 0);
   };
+  // Q^T operand of unit u, loaded while the current unit's state stays in
+  // place (its last softmax still needs it). Issued from inline asm like the
+  // K/V loads, so the compiler tracks none of the loop's global loads; the
+  // wait at the end of the softmax phase takes qreg as operands, so no use
+  // of qreg can move ahead of it.
+  auto load_q_of = [&](int u) __attribute__((always_inline)) {
+    int sg, tn, q0, lo, hi, hg;
+    unit(u, sg, tn, q0, lo, hi, hg);
+    const int kvh = hg / p.groups_per_kv;
+    const int hd = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + wave / p.rb;
+    const i32x4 rs = pp_rsrc_words(p.q + ((int64_t)sg * p.q_stride + (int64_t)hd * D) * 2, (uint32_t)tn * qst_b);
+    const uint32_t qa = (uint32_t)(q0 + (wave % p.rb) * 32 + lq) * qst_b + hf * 16;
+#pragma unroll
+    for (int i = 0; i < KST; ++i)
+      asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
+                   : "=v"(qreg[i]) : "v"(qa), "s"(rs), "n"(32 * i) : "memory");
+  };
 
   // ---- prologue: stream tiles 0 and 1 in flight, unit 0's Q ----
   // The compiler-visible wait for the Q loads also retires tile 0's loads;
@@ -302,28 +338,34 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   // LDS fragments are read two MFMA groups ahead of their use (V^T in two
   // register sets, K in a ring of three); sched_barriers keep the compiler
   // from sinking the reads next to their MFMAs.
-  auto vfrag = [&](const char* sV, int ks, f16x8* dst) __attribute__((always_inline)) {
+  auto vfrag = [&](uint32_t sv, int ks, f16x8* dst) __attribute__((always_inline)) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      const char* vp = sV + voff[db] + ks * 16 * S::ROW;
-      s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vp));
+      const uint32_t vp = va[db] + sv + ks * 16 * S::ROW;
+      s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(size_t)vp);
       s16x4 a2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(vp + 8 * S::ROW));
+          (__attribute__((address_space(3))) s16x4*)(size_t)(vp + 8 * S::ROW));
       f16x4 h1 = __builtin_bit_cast(f16x4, a1), h2 = __builtin_bit_cast(f16x4, a2);
       dst[db] = (f16x8){h1[0], h1[1], h1[2], h1[3], h2[0], h2[1], h2[2], h2[3]};
     }
   };
   // (u32x4 rather than bf16x8: register copies of bf16 vectors are split
   // into 16-bit halves and repacked.)
-  auto kfrag = [&](const char* sK, int st, u32x4* dst) __attribute__((always_inline)) {
+  auto kfrag = [&](uint32_t sk, int st, u32x4* dst) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) dst[kb] = *reinterpret_cast<const u32x4*>(sK + kb * 32 * S::ROW + koff[st]);
+    for (int kb = 0; kb < NKB; ++kb) dst[kb] = lds_load<u32x4>(ka[st] + sk + kb * 32 * S::ROW);
   };
-  // S^T = K Q^T with kr[0], kr[1] already holding the fragments of steps 0, 1.
-  auto qk_body = [&](const char* sK, u32x4 (*kr)[NKB]) __attribute__((always_inline)) {
+  // S^T = K Q^T with kr[0], kr[1] already holding the fragments of steps 0, 1;
+  // `mid()` runs after the MFMAs of step KST / 2. After every other step one
+  // MFMA adds a PV k-step's worth of the previous step's P to the row sum.
+  auto qk_body = [&](uint32_t sK, u32x4 (*kr)[NKB], auto&& mid) __attribute__((always_inline)) {
     const f32x16 zero = {};
 #pragma unroll
     for (int st = 0; st < KST; ++st) {
+      if (st == KST / 2 + 1) {
+        mid();
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (st + 2 < KST) kfrag(sK, st + 2, kr[(st + 2) % 3]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -331,16 +373,17 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
         sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[st % 3][kb]),
                                                            __builtin_bit_cast(bf16x8, qreg[st]),
                                                            st == 0 ? zero : sacc[kb], 0, 0, 0);
+
       __builtin_amdgcn_sched_barrier(0);
     }
   };
   // In-place bf16 -> fp16 of this wave's slice of V stage (exact below 65504
   // in magnitude): the reads are issued early, the conversion later.
-  auto conv_read = [&](const char* sV, u32x4* w) __attribute__((always_inline)) {
+  auto conv_read = [&](uint32_t sv, u32x4* w) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < S::KPW; ++i) w[i] = *reinterpret_cast<const u32x4*>(sV + cv_off[i]);
+    for (int i = 0; i < S::KPW; ++i) w[i] = lds_load<u32x4>(cv_a[i] + sv);
   };
-  auto conv_write = [&](char* sV, const u32x4* w) __attribute__((always_inline)) {
+  auto conv_write = [&](uint32_t sv, const u32x4* w) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < S::KPW; ++i) {
       u32x4 o;
@@ -349,7 +392,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
         f32x2 x = {__builtin_bit_cast(float, w[i][e] << 16), __builtin_bit_cast(float, w[i][e] & 0xffff0000u)};
         o[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2));
       }
-      *reinterpret_cast<u32x4*>(sV + cv_off[i]) = o;
+      lds_store<u32x4>(cv_a[i] + sv, o);
     }
   };
 
@@ -399,26 +442,23 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   };
 
   // ---- MFMA phase of the stream step whose K and V are in stage `st` ----
-  // O^T += V^T P^T of the previous step (stage st - 1), the store of a
-  // finished unit's output (fin), S^T = K Q^T of this step, and the
-  // conversion of this wave's slice of this step's V. Fragment reads for the
-  // first MFMAs go out first, then the reads of the V slice to convert; the
-  // conversion itself sits between PV k-steps. Every product is computed on
+  // O^T += V^T P^T of the previous step (stage st - 1) and its row sum,
+  // S^T = K Q^T of this step, the conversion of this wave's slice of this
+  // step's V, and at the end the store of a finished unit's output (fin). Every product is computed on
   // every step: tiles (or rows) a wave does not see are masked to P = 0 by
   // the softmax, which costs less than branching around them. LAST: the
   // step after the stream's end, PV and store only.
   bool fin = false;
   auto mphase = [&](auto last_tag, uint32_t st) __attribute__((always_inline)) {
     constexpr bool LAST = decltype(last_tag)::value;
-    const char* sK = sKb + st;
-    char* sVc = sVb + st;
-    const char* sV = sVb + ((st + (S::STAGES - 1) * S::TILE) & (S::STAGES * S::TILE - 1));
+    const uint32_t sK = st;
+    const uint32_t sVc = st;
+    const uint32_t sV = (st + (S::STAGES - 1) * S::TILE) & (S::STAGES * S::TILE - 1);
     u32x4 w[S::KPW];
     u32x4 kr[3][NKB];
     f16x8 vs[2][NDB];
     vfrag(sV, 0, vs[0]);
     vfrag(sV, 1, vs[1]);
-    if (!LAST) conv_read(sVc, w);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < PKS; ++ks) {
@@ -430,14 +470,16 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       if (ks + 2 < PKS) vfrag(sV, ks + 2, vs[ks & 1]);
       if (!LAST && ks + 2 >= PKS) kfrag(sK, ks + 2 - PKS, kr[ks + 2 - PKS]);
       __builtin_amdgcn_sched_barrier(0);
-      if (!LAST && ks == 1) conv_write(sVc, w);
-      __builtin_amdgcn_sched_barrier(0);
     }
+    // The V slice to convert is read behind the first K fragments and written
+    // back during QK^T, so that waiting for it never holds up an MFMA.
+    if (!LAST) conv_read(sVc, w);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!LAST) qk_body(sK, kr, [&]() __attribute__((always_inline)) { conv_write(sVc, w); });
     if (__builtin_expect(fin, 0)) {
       store_out();
       fin = false;
     }
-    if (!LAST) qk_body(sK, kr);
   };
 
   // P (fp16) and its per-lane sum over this tile, with reference max `base`.
@@ -489,24 +531,31 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   // before the row max (which waits for the last QK^T MFMAs), the others
   // between P's k-steps. On the unit's last tile the next unit's Q is loaded
   // too and the cursor moves on. At the end the wave waits for the loads it
-  // issued one phase earlier, which the next MFMA phases read (all of its
-  // loads, when it moved to a new unit). Returns false after the stream's
-  // last tile.
+  // issued one phase earlier, which the next MFMA phases read. Sets `done`
+  // after the stream's last tile.
   int t = lo_t;
+  bool done = false;
   auto vphase = [&](uint32_t dst) __attribute__((always_inline)) {
+    // On a unit's last tile the next unit's Q goes out first: the loads
+    // issued after it (this phase's K/V) then need not land before the
+    // wait at the end of the phase covers the Q loads.
+    if (__builtin_expect(t + 1 == hi_t && cu + 1 < nu, 0)) load_q_of(cu + 1);
     dma_part(0, dst);
     __builtin_amdgcn_sched_barrier(0);
     if (__builtin_expect((uint32_t)(t - f_lo) >= (uint32_t)f_n, 0)) apply_mask(t);
-    // Row max (v_maximum3: no NaN canonicalisation), across the two halves.
-    float mx4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    // Row max (v_maximum3: no NaN canonicalisation), across the two halves:
+    // four chains over 8 values each, every v_maximum3 taking two new ones.
+    auto mx2 = [](float a, float b) __attribute__((always_inline)) { return __builtin_elementwise_maximum(a, b); };
+    float ch[4];
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2)
-        mx4[(kb * 8 + r / 2) & 3] = __builtin_elementwise_maximum(
-            mx4[(kb * 8 + r / 2) & 3], __builtin_elementwise_maximum(sacc[kb][r], sacc[kb][r + 1]));
-    float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx4[0], mx4[1]),
-                                             __builtin_elementwise_maximum(mx4[2], mx4[3]));
+    for (int c = 0; c < 4; ++c) {
+      const int kb = c >> 1, o = 8 * (c & 1);
+      float m = mx2(sacc[kb][o], sacc[kb][o + 1]);
+      m = mx2(mx2(m, sacc[kb][o + 2]), sacc[kb][o + 3]);
+      m = mx2(mx2(m, sacc[kb][o + 4]), sacc[kb][o + 5]);
+      ch[c] = mx2(mx2(m, sacc[kb][o + 6]), sacc[kb][o + 7]);
+    }
+    float mx = mx2(mx2(mx2(ch[0], ch[1]), ch[2]), ch[3]);
     mx = half_max(mx) * c2;
     // Lazy rescaling: the reference max moves only when a row's max grows by
     // more than 2^8 (P then stays <= 256, well inside fp16's range).
@@ -537,17 +586,17 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       fin = true;
       if (cu + 1 < nu) {
         set_unit(++cu);
-        t = lo_t;
-        load_q();
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        return true;
+        t = lo_t - 1;
+      } else {
+        done = true;
       }
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::KPW) : "memory");
-      return false;
     }
     ++t;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S::KPW) : "memory");
-    return true;
+    static_assert(KST == 8, "the wait below names eight Q registers");
+    asm volatile("s_waitcnt vmcnt(%8)"
+                 : "+v"(qreg[0]), "+v"(qreg[1]), "+v"(qreg[2]), "+v"(qreg[3]), "+v"(qreg[4]), "+v"(qreg[5]),
+                   "+v"(qreg[6]), "+v"(qreg[7])
+                 : "n"(2 * S::KPW) : "memory");
   };
 
   // ---- the stream, in barrier-separated half-slots ----
@@ -560,9 +609,9 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     mphase(std::false_type{}, SI * S::TILE);
     lds_barrier();
     const uint32_t dst = grp ? ((SI + 3) & 3) * S::TILE : ((SI + 2) & 3) * S::TILE;
-    const bool more = vphase(dst);
+    vphase(dst);
     lds_barrier();
-    return more;
+    return !done;
   };
   if (grp) {
     dma_tile(2 * S::TILE);
