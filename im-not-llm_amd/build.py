@@ -10,6 +10,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -20,18 +22,36 @@ INCLUDE = PKG.parent / "include"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-# Packed fp32 VALU ops are disabled for all device code (see DESIGN notes on
-# the pool's packed-fp32 hazards); hipcc's host pass warns that it does not
-# know the feature, which is harmless.
+# Packed fp32 VALU instructions (v_pk_fma_f32 and the like) are disabled for
+# all device code: some of their forms have produced wrong results without
+# any error on these GPUs. hipcc's host pass warns that it does not know the
+# feature, which is harmless.
 FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", f"-I{INCLUDE}",
 ]
+LINK_FLAGS = [f"--offload-arch={ARCH}", "-shared", "-fPIC"]
+
+
+# Per-source flags. attn_wide.hip (head_dim 256, one wave per SIMD, ~450 of
+# 512 registers): MFMA accumulators in VGPRs, so that O^T, which the softmax
+# rescales with VALU instructions, is not copied between AGPRs and VGPRs on
+# every tile; the MFMA operands then take the AGPRs.
+EXTRA = {
+    "attn_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def sources():
     return sorted(CSRC.glob("*.hip"))
+
+
+def _run(cmd):
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    return res.returncode, err
 
 
 def build(verbose: bool = False) -> Path:
@@ -39,14 +59,22 @@ def build(verbose: bool = False) -> Path:
     if not Path(HIPCC).exists() and shutil.which(HIPCC) is None:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     tmp = OUT.with_suffix(".so.tmp")
-    cmd = [HIPCC, *FLAGS, *map(str, sources()), "-o", str(tmp)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+    with tempfile.TemporaryDirectory(prefix="inl_hip_build_") as objdir:
+        jobs = []
+        for src in sources():
+            obj = Path(objdir) / (src.stem + ".o")
+            cmd = [HIPCC, *FLAGS, "-c", *EXTRA.get(src.name, []), str(src), "-o", str(obj)]
+            jobs.append((src, obj, cmd))
+        with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1, 8)) as pool:
+            results = list(pool.map(lambda j: _run(j[2]), jobs))
+        for (src, _, _), (rc, err) in zip(jobs, results):
+            if rc != 0:
+                raise RuntimeError(f"hipcc failed on {src.name} ({rc}):\n{err}")
+            if verbose and err.strip():
+                print(err, file=sys.stderr)
+        rc, err = _run([HIPCC, *LINK_FLAGS, *(str(o) for _, o, _ in jobs), "-o", str(tmp)])
+        if rc != 0:
+            raise RuntimeError(f"hipcc link failed ({rc}):\n{err}")
     os.replace(tmp, OUT)
     return OUT
 

@@ -438,7 +438,7 @@ int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, bool fits32, K
   if (dtype == INL_BF16 && pv16 && fits32) {
     AttnKernelFn fn;
     int bn, nw, lds;
-    if (bf16_pp_kernel(head_dim, &fn, &bn, &nw, &lds)) {
+    if (bf16_pp_kernel(head_dim, &fn, &bn, &nw, &lds) || bf16_wide_kernel(head_dim, &fn, &bn, &nw, &lds)) {
       *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true};
       return INL_OK;
     }

@@ -70,4 +70,8 @@ bool bf16_fast_kernel(int head_dim_padded, AttnKernelFn* fn, int* bn, int* nw, i
 constexpr int PP_MAX_UNITS = 1024;
 bool bf16_pp_kernel(int head_dim, AttnKernelFn* fn, int* bn, int* nw, int* lds);
 
+// Persistent bf16 kernel for head_dim 256 (attn_wide.hip): 4 waves, one per
+// SIMD, each overlapping its softmax with its own MFMAs; same unit lists.
+bool bf16_wide_kernel(int head_dim, AttnKernelFn* fn, int* bn, int* nw, int* lds);
+
 }  // namespace inl
