@@ -206,7 +206,8 @@ def main():
     hbm_bytes = tokens * (2 * hq * d + 2 * 2 * hkv * d + 2 * hq * d)
     bn = plans[0].info()["block_n"]
     kernel = (f"attn_pp_kernel<{d}, {bn}>" if d == 128
-              else f"attn_bf16_kernel<{d}, {bn}, 4>" if d in (64, 256)
+              else f"attn_wide_kernel<{d}, {bn}>" if d == 256
+              else f"attn_bf16_kernel<{d}, {bn}, 4>" if d == 64
               else f"attn_fwd_kernel<bf16, {d}, {bn}>")
     n_launch = len(batches)
     stream = torch.cuda.current_stream()
