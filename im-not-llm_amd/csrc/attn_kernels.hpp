@@ -41,6 +41,10 @@ __device__ __forceinline__ void swap_halves(float x, float* a, float* b) {
   *a = u;
   *b = v;
 }
+// Lanes 32-63 of a trade places with lanes 0-31 of b.
+__device__ __forceinline__ void swap_lanes_32(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
 __device__ __forceinline__ float half_max(float x) {
   float a, b;
   swap_halves(x, &a, &b);

@@ -67,7 +67,6 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   constexpr int PKS = BN / 16;   // k-steps of the PV product
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  char* const sKb = smem;
   char* const sVb = smem + S::STAGES * S::TILE;
   const uint32_t lds0 = lds_addr(smem);
 
@@ -227,18 +226,24 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   // K/V loads, so the compiler tracks none of the loop's global loads; the
   // wait at the end of the softmax phase takes qreg as operands, so no use
   // of qreg can move ahead of it.
-  auto load_q_of = [&](int u) __attribute__((always_inline)) {
+  auto q_addr = [&](int u, i32x4& rs, uint32_t& qa) __attribute__((always_inline)) {
     int sg, tn, q0, lo, hi, hg;
     unit(u, sg, tn, q0, lo, hi, hg);
     const int kvh = hg / p.groups_per_kv;
     const int hd = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + wave / p.rb;
-    const i32x4 rs = pp_rsrc_words(p.q + ((int64_t)sg * p.q_stride + (int64_t)hd * D) * 2, (uint32_t)tn * qst_b);
-    const uint32_t qa = (uint32_t)(q0 + (wave % p.rb) * 32 + lq) * qst_b + hf * 16;
+    rs = pp_rsrc_words(p.q + ((int64_t)sg * p.q_stride + (int64_t)hd * D) * 2, (uint32_t)tn * qst_b);
+    qa = (uint32_t)(q0 + (wave % p.rb) * 32 + lq) * qst_b + hf * 16;
+  };
+  auto load_q_of = [&](int u) __attribute__((always_inline)) {
+    i32x4 rs;
+    uint32_t qa;
+    q_addr(u, rs, qa);
 #pragma unroll
     for (int i = 0; i < KST; ++i)
       asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
                    : "=v"(qreg[i]) : "v"(qa), "s"(rs), "n"(32 * i) : "memory");
   };
+
 
   // ---- prologue: stream tiles 0 and 1 in flight, unit 0's Q ----
   // The compiler-visible wait for the Q loads also retires tile 0's loads;
@@ -334,42 +339,70 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     }
   };
 
-  // Output of the unit whose O^T is accumulating: o_row points at this
-  // lane's first output column (4 * hf) of its query row, so the columns a
-  // lane stores are o_row + compile-time offsets. Captured when the compute
-  // cursor leaves the unit; stored after the unit's last PV.
-  char* o_row = nullptr;
-  bool o_valid = false;
+  // Output of the unit whose O^T is accumulating, captured when the compute
+  // cursor leaves the unit and stored after the unit's last PV. The stores
+  // go through a buffer descriptor that ends at the text's last row, so the
+  // hardware drops the rows past it (and whole waves past it) without a
+  // branch.
+  __amdgpu_buffer_rsrc_t ors;
+  uint32_t o_off = 0;
+  const uint32_t ost_b = (uint32_t)(p.o_stride * osz);
   auto capture_out = [&]() __attribute__((always_inline)) {
-    const int qrow = r0 + lq;
-    o_valid = active && qrow < T;
-    o_row = p.o + ((int64_t)(seg + (o_valid ? qrow : 0)) * p.o_stride + (int64_t)head * D + 4 * hf) * osz;
+    ors = pp_rsrc(p.o + ((int64_t)seg * p.o_stride + (int64_t)head * D) * osz, (uint32_t)T * ost_b);
+    // bf16: row lane / 8 (+ 8 j), 16-byte chunk lane % 8 of a 128-byte
+    // half-row; f32: this lane's query row, first column 16 bytes * hf.
+    o_off = p.out_bf16 ? (uint32_t)(r0 + (lane >> 3)) * ost_b + 16 * (lane & 7)
+                       : (uint32_t)(r0 + lq) * ost_b + 16 * hf;
   };
-  auto store_out = [&]() __attribute__((always_inline)) {
+  // O^T element (db, 4 g + e) of lane (lq, hf) is output column
+  // db * 32 + 8 g + 4 hf + e. For bf16, one v_permlane32_swap per register
+  // pair gives lane hf = 0 columns 16 q .. 16 q + 7 and lane hf = 1 columns
+  // 16 q + 8 .. 16 q + 15 of 16-column group q (16 contiguous bytes, chunk
+  // 2 q + hf of the row). The wave then transposes its 32 rows through LDS,
+  // one 128-byte half-row at a time (chunk c of row r at r * 128 +
+  // ((c ^ (r & 7)) << 4)), so that each store writes 8 whole 128-byte lines.
+  // `stg`: 4 KB of LDS that no other wave touches during this phase.
+  auto store_out = [&](uint32_t stg) __attribute__((always_inline)) {
     const float l_tot = half_sum(l_i);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (o_valid) {
-      if (p.out_bf16) {
+    if (p.out_bf16) {
+      u32x4 ch[2 * NDB];
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            bf16x4 val;
+        for (int gp = 0; gp < 2; ++gp) {
+          uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) val[e] = (bf16)(oacc[db][4 * g + e] * inv);
-            *reinterpret_cast<bf16x4*>(o_row + (db * 32 + 8 * g) * 2) = val;
+          for (int h = 0; h < 4; ++h) {
+            const f32x2 x = {oacc[db][8 * gp + 2 * h] * inv, oacc[db][8 * gp + 2 * h + 1] * inv};
+            w[h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
           }
-      } else {
+          swap_lanes_32(w[0], w[2]);
+          swap_lanes_32(w[1], w[3]);
+          ch[2 * db + gp] = (u32x4){w[0], w[1], w[2], w[3]};
+        }
+      const uint32_t wr = stg + lq * 128;
+      const uint32_t rrow = lane >> 3;
+      const uint32_t rd = stg + rrow * 128 + (((lane & 7) ^ (rrow & 7)) << 4);
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+      for (int half = 0; half < 2; ++half) {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            f32x4 val;
+        for (int i = 0; i < 4; ++i) lds_store<u32x4>(wr + (((2 * i + hf) ^ (lq & 7)) << 4), ch[4 * half + i]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e] * inv;
-            *reinterpret_cast<f32x4*>(o_row + (db * 32 + 8 * g) * 4) = val;
-          }
+        for (int j = 0; j < 4; ++j)
+          __builtin_amdgcn_raw_buffer_store_b128(lds_load<u32x4>(rd + j * 8 * 128), ors,
+                                                 o_off + j * 8 * ost_b + half * 128, 0, 0);
       }
+    } else {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x4 val;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) val[e] = __builtin_bit_cast(uint32_t, oacc[db][4 * g + e] * inv);
+          __builtin_amdgcn_raw_buffer_store_b128(val, ors, o_off + (db * 32 + 8 * g) * 4, 0, 0);
+        }
     }
 #pragma unroll
     for (int i = 0; i < NDB; ++i)
@@ -415,7 +448,9 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     __builtin_amdgcn_sched_barrier(0);
     if (!LAST) qk_body(sK, kr, [&]() __attribute__((always_inline)) { conv_write(sVc, w); });
     if (__builtin_expect(fin, 0)) {
-      store_out();
+      // The K half of stage st - 1: both groups' QK^T of that tile are done,
+      // and its next load is issued after this tile's MFMA phases.
+      store_out(lds0 + ((st + (S::STAGES - 1) * S::TILE) & (S::STAGES * S::TILE - 1)) + (wave & 3) * 4096);
       fin = false;
     }
   };
@@ -451,15 +486,25 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     const int kbase = kt0 + 4 * hf;
     const int dT = T - kbase;                     // key < T     <=> c < dT
     const int dq = r0 + lq - kbase;               // key <= qi   <=> c <= dq
-    const int whi = window >= 0 ? dq + window : 0x7fffffff;            // c <= whi
-    const int wlo = window >= 0 ? dq - window : -0x7fffffff;           // c >= wlo
-    const int chi = min(causal ? dq : 0x7fffffff, min(dT - 1, whi));   // c <= chi
+    // lo <= c <= hi (lo: the window of the last row; hi: the text end, the
+    // causal diagonal and the window of the first row) as one unsigned
+    // comparison, c - lo <= hi - lo; an empty range becomes lo = 2^30, where
+    // c - lo wraps above any span. Without a window lo = 0 (c >= 0 anyway).
+    int hi = min(causal ? dq : 0x7fffffff, dT - 1);
+    int lo = 0;
+    if (window >= 0) {
+      hi = min(hi, dq + window);
+      lo = max(0, dq - window);
+    }
+    const bool none = hi < lo;
+    const uint32_t span = none ? 0u : (uint32_t)(hi - lo);
+    lo = none ? (1 << 30) : lo;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int c = kb * 32 + 8 * (r >> 2) + (r & 3);
-        sacc[kb][r] = (c <= chi && c >= wlo) ? sacc[kb][r] : -INFINITY;
+        sacc[kb][r] = (uint32_t)(c - lo) <= span ? sacc[kb][r] : -INFINITY;
       }
   };
 
@@ -530,6 +575,10 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       }
     }
     ++t;
+    // Loads retire from vmcnt in issue order, stores independently of
+    // them: with at most 2 * KPW ops in flight, every load older than this
+    // phase's K/V loads (the Q loads among them) is done, whatever the
+    // stores do.
     static_assert(KST == 8, "the wait below names eight Q registers");
     asm volatile("s_waitcnt vmcnt(%8)"
                  : "+v"(qreg[0]), "+v"(qreg[1]), "+v"(qreg[2]), "+v"(qreg[3]), "+v"(qreg[4]), "+v"(qreg[5]),
