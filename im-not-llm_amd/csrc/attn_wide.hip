@@ -266,52 +266,88 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
                                                     __builtin_bit_cast(bf16x8, qreg[st]), st == 0 ? zero : acc, 0, 0, 0);
   };
 
+  // Key of element r is kbase + c with c a compile-time offset. lo <= c <= hi
+  // (lo: the window of the last row; hi: the text end, the causal diagonal
+  // and the window of the first row) as one unsigned comparison,
+  // c - lo <= hi - lo; an empty range becomes lo = 2^30, where c - lo wraps
+  // above any span. Without a window lo = 0 (c >= 0 anyway).
   auto apply_mask = [&](f32x16& s, int j) __attribute__((always_inline)) {
     const int kbase = j * BN + 4 * hf;
     const int dT = T - kbase;
     const int dq = r0 + lq - kbase;
-    const int whi = window >= 0 ? dq + window : 0x7fffffff;
-    const int wlo = window >= 0 ? dq - window : -0x7fffffff;
-    const int chi = min(causal ? dq : 0x7fffffff, min(dT - 1, whi));
+    int hi = min(causal ? dq : 0x7fffffff, dT - 1);
+    int lo = 0;
+    if (window >= 0) {
+      hi = min(hi, dq + window);
+      lo = max(0, dq - window);
+    }
+    const bool none = hi < lo;
+    const uint32_t span = none ? 0u : (uint32_t)(hi - lo);
+    lo = none ? (1 << 30) : lo;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int c = 8 * (r >> 2) + (r & 3);
-      s[r] = (c <= chi && c >= wlo) ? s[r] : -INFINITY;
+      s[r] = (uint32_t)(c - lo) <= span ? s[r] : -INFINITY;
     }
   };
 
-  char* o_row = nullptr;
-  bool o_valid = false;
+  // The stores go through a buffer descriptor that ends at the text's last
+  // row, so the hardware drops the rows past it without a branch.
+  __amdgpu_buffer_rsrc_t ors;
+  uint32_t o_off = 0;
+  const uint32_t ost_b = (uint32_t)(p.o_stride * osz);
   auto capture_out = [&]() __attribute__((always_inline)) {
-    const int qrow = r0 + lq;
-    o_valid = active && qrow < T;
-    o_row = p.o + ((int64_t)(seg + (o_valid ? qrow : 0)) * p.o_stride + (int64_t)head * D + 4 * hf) * osz;
+    ors = pp_rsrc(p.o + ((int64_t)seg * p.o_stride + (int64_t)head * D) * osz, (uint32_t)T * ost_b);
+    // bf16: row lane / 8 (+ 8 j), 16-byte chunk lane % 8 of a 128-byte
+    // quarter row; f32: this lane's query row, first column 16 bytes * hf.
+    o_off = p.out_bf16 ? (uint32_t)(r0 + (lane >> 3)) * ost_b + 16 * (lane & 7)
+                       : (uint32_t)(r0 + lq) * ost_b + 16 * hf;
   };
-  auto store_out = [&]() __attribute__((always_inline)) {
+  // O^T element (db, 4 g + e) of lane (lq, hf) is output column
+  // db * 32 + 8 g + 4 hf + e. For bf16, one v_permlane32_swap per register
+  // pair gives lane hf = 0 columns 16 q .. 16 q + 7 and lane hf = 1 columns
+  // 16 q + 8 .. 16 q + 15 (16 contiguous bytes, chunk 2 q + hf of the row).
+  // The wave then transposes its 32 rows through LDS, one 128-byte quarter
+  // row at a time (chunk c of row r at r * 128 + ((c ^ (r & 7)) << 4)), so
+  // that each store writes 8 whole 128-byte lines. `stg`: 4 KB of LDS that
+  // no other wave touches during this step.
+  auto store_out = [&](uint32_t stg) __attribute__((always_inline)) {
     const float l_tot = half_sum(l_i);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (o_valid) {
-      if (p.out_bf16) {
+    if (p.out_bf16) {
+      const uint32_t wr = stg + lq * 128;
+      const uint32_t rrow = lane >> 3;
+      const uint32_t rd = stg + rrow * 128 + (((lane & 7) ^ (rrow & 7)) << 4);
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+      for (int part = 0; part < NDB / 2; ++part) {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            bf16x4 val;
+        for (int i = 0; i < 4; ++i) {
+          const int db = 2 * part + (i >> 1), gp = i & 1;
+          uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) val[e] = (bf16)(oacc[db][4 * g + e] * inv);
-            *reinterpret_cast<bf16x4*>(o_row + (db * 32 + 8 * g) * 2) = val;
+          for (int h = 0; h < 4; ++h) {
+            const f32x2 x = {oacc[db][8 * gp + 2 * h] * inv, oacc[db][8 * gp + 2 * h + 1] * inv};
+            w[h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
           }
-      } else {
+          swap_lanes_32(w[0], w[2]);
+          swap_lanes_32(w[1], w[3]);
+          lds_store<u32x4>(wr + (((2 * i + hf) ^ (lq & 7)) << 4), (u32x4){w[0], w[1], w[2], w[3]});
+        }
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            f32x4 val;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e] * inv;
-            *reinterpret_cast<f32x4*>(o_row + (db * 32 + 8 * g) * 4) = val;
-          }
+        for (int j = 0; j < 4; ++j)
+          __builtin_amdgcn_raw_buffer_store_b128(lds_load<u32x4>(rd + j * 8 * 128), ors,
+                                                 o_off + j * 8 * ost_b + part * 128, 0, 0);
       }
+    } else {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x4 val;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) val[e] = __builtin_bit_cast(uint32_t, oacc[db][4 * g + e] * inv);
+          __builtin_amdgcn_raw_buffer_store_b128(val, ors, o_off + (db * 32 + 8 * g) * 4, 0, 0);
+        }
     }
 #pragma unroll
     for (int i = 0; i < NDB; ++i)
@@ -466,7 +502,9 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
     // the softmax / PV cursor moves to tile j + 1
     if (__builtin_expect(t + 1 == hi_t, 0)) {
       capture_out();
-      store_out();
+      // The K half of this step's stage: its QK^T ran in the previous step,
+      // and its next load is issued in the next one.
+      store_out(lds0 + st_cur + wave * 4096);
       if (cu + 1 < nu) {
         set_unit(++cu);
         t = lo_t - 1;
