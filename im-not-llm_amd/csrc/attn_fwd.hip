@@ -424,6 +424,7 @@ struct KernelCfg {
   int lds;      // dynamic LDS bytes
   int rows;     // query rows per wave (32 or 64)
   bool persistent = false;  // one workgroup per CU over a host-assigned unit list
+  bool head_pairs = false;  // a unit serves two query heads with their own K/V (group 1)
 };
 
 template <typename E, int D, int BN, int NW, bool PV16>
@@ -433,11 +434,16 @@ KernelCfg make_cfg() {
 
 // `fits32`: every text's q/k/v rows span < 4 GiB, as the fast kernel's
 // 32-bit buffer offsets need.
-int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, bool fits32, KernelCfg* cfg) {
+int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, bool fits32, int h_q, int group,
+                  KernelCfg* cfg) {
   const bool pv16 = !(flags & INL_ATTN_PV_BF16);
   if (dtype == INL_BF16 && pv16 && fits32) {
     AttnKernelFn fn;
     int bn, nw, lds;
+    if (group == 1 && h_q % 2 == 0 && bf16_pp64_kernel(head_dim, &fn, &bn, &nw, &lds)) {
+      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true, true};
+      return INL_OK;
+    }
     if (bf16_pp_kernel(head_dim, &fn, &bn, &nw, &lds) || bf16_wide_kernel(head_dim, &fn, &bn, &nw, &lds)) {
       *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true};
       return INL_OK;
@@ -616,12 +622,19 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
   const int64_t vs = d->v_row_stride ? d->v_row_stride : (int64_t)d->h_kv * d->head_dim;
   const int64_t widest = std::max(qs, std::max(ks, vs)) * es;
   const bool fits32 = (max_t + 256) * widest < ((int64_t)1 << 32);
-  int rc = select_kernel(d->dtype, d->head_dim, d->flags, fits32, &s->cfg);
+  int rc = select_kernel(d->dtype, d->head_dim, d->flags, fits32, d->h_q, d->h_q / d->h_kv, &s->cfg);
   if (rc) return rc;
   const int group = d->h_q / d->h_kv;
-  s->hpw = heads_per_wg(group, s->cfg.nw);
-  s->n_hg = d->h_kv * (group / s->hpw);
-  s->block_m = s->cfg.rows * (s->cfg.nw / s->hpw);
+  if (s->cfg.head_pairs) {
+    // two heads per unit, one per wave group: 4 waves x 32 rows
+    s->hpw = 2;
+    s->n_hg = d->h_q / 2;
+    s->block_m = s->cfg.rows * (s->cfg.nw / 2);
+  } else {
+    s->hpw = heads_per_wg(group, s->cfg.nw);
+    s->n_hg = d->h_kv * (group / s->hpw);
+    s->block_m = s->cfg.rows * (s->cfg.nw / s->hpw);
+  }
   const int BM = s->block_m, BN = s->cfg.bn;
   std::vector<CostedItem> tmp;
   for (int b = 0; b < d->n_texts; ++b) {
@@ -668,7 +681,7 @@ AttnParams make_params(const inl_attn_desc* d, const Schedule& s, const void* de
   p.wg_start = (const int32_t*)((const char*)dev_sched + s.wg_offset());
   p.group = d->h_q / d->h_kv;
   p.hpw = s.hpw;
-  p.groups_per_kv = p.group / s.hpw;
+  p.groups_per_kv = s.cfg.head_pairs ? 1 : p.group / s.hpw;
   p.n_hg = s.n_hg;
   p.rb = s.cfg.nw / s.hpw;
   p.head_dim = d->head_dim;

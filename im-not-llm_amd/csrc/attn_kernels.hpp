@@ -78,4 +78,8 @@ bool bf16_pp_kernel(int head_dim, AttnKernelFn* fn, int* bn, int* nw, int* lds);
 // SIMD, each overlapping its softmax with its own MFMAs; same unit lists.
 bool bf16_wide_kernel(int head_dim, AttnKernelFn* fn, int* bn, int* nw, int* lds);
 
+// Persistent ping-pong kernel for head_dim 64 without grouped queries: each
+// unit serves two query heads, one per wave group (attn_pp64.hip).
+bool bf16_pp64_kernel(int head_dim, AttnKernelFn* fn, int* bn, int* nw, int* lds);
+
 }  // namespace inl
