@@ -1,0 +1,177 @@
+"""Tiny-checkpoint encoders for the reference's HF golden fixtures (test
+infrastructure).
+
+The fixtures under ``tests/golden/<name>/`` are the reference's own test data
+(a tiny random ``model.safetensors``, its ``config.json`` and
+``tokenizer.json``, and the ``golden.json`` vectors HF ``transformers``
+produced for them). The encoders below run the whole tiny model in numpy,
+following the reference's forward pass, and route the ops of the attention
+hot path (per-head RMSNorm + RoPE, packed varlen attention, pooling, L2) to
+an ``ops`` object: the numpy oracle (``OracleOps``) or the HIP library through
+its C ABI (``HipOps``). Everything else (projections, MLP, embeddings) stays
+in numpy f64.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+
+from oracle import attention as oa
+from oracle import pooling as opool
+from oracle import prologue as opro
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def load_fixture(name: str):
+    """(config dict, f64 weights dict, golden dict, tokenizer directory)."""
+    from safetensors.numpy import load_file
+    d = GOLDEN / name
+    cfg = json.loads((d / "config.json").read_text())
+    weights = {k: v.astype(np.float64) for k, v in load_file(str(d / "model.safetensors")).items()}
+    golden = json.loads((d / "golden.json").read_text())
+    return cfg, weights, golden, d
+
+
+def tokenize(fixture_dir: Path, texts, max_length: int):
+    """Token ids per text: the fixture's tokenizer with its post-processor
+    (special tokens) and truncation to ``max_length``, no padding (rows are
+    packed)."""
+    import tokenizers
+    tok = tokenizers.Tokenizer.from_file(str(fixture_dir / "tokenizer.json"))
+    tok.enable_truncation(max_length)
+    return [e.ids for e in tok.encode_batch(list(texts))]
+
+
+def gelu_tanh(x):
+    """candle ``Tensor::gelu`` (the tanh approximation, ``gelu_pytorch_tanh``)."""
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+class OracleOps:
+    """The hot-path ops as the numpy oracle computes them (f64)."""
+
+    def norm_rope(self, x, weight, eps, table=None, pos=None):
+        y = opro.rms_norm(x, weight, eps)
+        if table is not None:
+            cos, sin = table
+            y = opro.rope(y, cos[pos][:, None, :].astype(np.float64), sin[pos][:, None, :].astype(np.float64))
+        return y
+
+    def attention(self, q, k, v, cu, *, causal, window, scale):
+        return oa.varlen_attention(q, k, v, cu, causal=causal, window=window, scale=scale)
+
+    def mean_pool(self, h, cu):
+        return opool.mean_pool(h, cu)
+
+    def l2(self, x):
+        return opool.l2_normalize(x)
+
+
+class HipOps:
+    """The same ops through the HIP library in f32 (device tensors in and out
+    of each call; the numpy glue converts)."""
+
+    def __init__(self, inl, torch, device):
+        self.inl, self.torch, self.dev = inl, torch, device
+        self._tables = {}
+
+    def _t(self, x):
+        return self.torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(self.dev)
+
+    def norm_rope(self, x, weight, eps, table=None, pos=None):
+        w = self._t(weight) if weight is not None else None
+        kw = {}
+        if table is not None:
+            cos, sin = table
+            kw = dict(rows=self.torch.from_numpy(np.ascontiguousarray(pos, dtype=np.int32)).to(self.dev),
+                      cos=self._t(cos), sin=self._t(sin))
+        y = self.inl.norm_rope(self._t(x), weight=w, eps=eps, **kw)
+        return y.cpu().numpy().astype(np.float64)
+
+    def attention(self, q, k, v, cu, *, causal, window, scale):
+        o = self.inl.varlen_attention(self._t(q), self._t(k), self._t(v), [int(c) for c in cu],
+                                      causal=causal, window=window, scale=scale)
+        return o.cpu().numpy().astype(np.float64)
+
+    def mean_pool(self, h, cu):
+        cu_d = self.torch.from_numpy(np.ascontiguousarray(cu, dtype=np.int32)).to(self.dev)
+        return self.inl.pool_mean(self._t(h), cu_d).cpu().numpy().astype(np.float64)
+
+    def l2(self, x):
+        return self.inl.l2_normalize(self._t(x)).cpu().numpy().astype(np.float64)
+
+
+def _positions(lens):
+    return np.concatenate([np.arange(n) for n in lens]) if lens else np.zeros(0, dtype=np.int64)
+
+
+# ---------------------------------------------------------------------------
+# EmbeddingGemma 2 (crates/inl-text/src/gemma2.rs)
+# ---------------------------------------------------------------------------
+
+def gemma2_embed(fixture, texts, max_length: int, ops):
+    """Unit-length embeddings ``[B, embedding_dim]``, following
+    gemma2.rs:606-662 (embedding scale, per-layer inputs, layers, final norm,
+    mean over real tokens, projection, L2) with the layer of :473-496, the
+    attention of :381-441 (per-head q/k RMSNorm + RoPE, weightless v norm,
+    scale 1, sliding layers masked to ``|q - k| <= sliding_window``) and the
+    per-layer-input block of :279-283. Rows are packed; the reference right
+    pads them and masks the padding, which is the same function for the real
+    rows."""
+    cfg, W, _, fdir = fixture
+    tc = cfg["text_config"]
+    ids = tokenize(fdir, texts, max_length)
+    lens = [len(x) for x in ids]
+    cu = oa.cu_from_lengths(lens)
+    flat = np.concatenate([np.asarray(x, dtype=np.int64) for x in ids])
+    pos = _positions(lens)
+    hs, eps = tc["hidden_size"], tc["rms_norm_eps"]
+    n_layers, ple_dim = tc["num_hidden_layers"], tc["hidden_size_per_layer_input"]
+    p = "language_model."
+
+    def lin(x, name):
+        return x @ W[p + name + ".weight"].T
+
+    def layer_shape(i):
+        over = tc.get("per_layer_config", {}).get(f"{i:02d}", {})
+        return (tc["layer_types"][i], over.get("head_dim", tc["head_dim"]),
+                over.get("num_key_value_heads", tc["num_key_value_heads"]))
+
+    positions = max(lens) if lens else 1
+    tables = {}
+    for kind, key in (("sliding_attention", "sliding_attention"), ("full_attention", "full_attention")):
+        hd = next((layer_shape(i)[1] for i in range(n_layers) if layer_shape(i)[0] == kind), tc["head_dim"])
+        tables[kind] = opro.rope_table(hd, tc["rope_parameters"][key]["rope_theta"], positions)
+
+    h = W[p + "embed_tokens.weight"][flat] * np.sqrt(float(hs))
+    per_layer = (lin(h, "ple.per_layer_model_projection") * hs ** -0.5).reshape(-1, n_layers, ple_dim)
+    per_layer = opro.rms_norm(per_layer, W[p + "ple.per_layer_projection_norm.weight"], eps)
+    heads = tc["num_attention_heads"]
+    n = h.shape[0]
+    for i in range(n_layers):
+        kind, hd, kvh = layer_shape(i)
+        lp = f"layers.{i}."
+        x = opro.rms_norm(h, W[p + lp + "input_layernorm.weight"], eps)
+        q = lin(x, lp + "self_attn.q_proj").reshape(n, heads, hd)
+        k = lin(x, lp + "self_attn.k_proj").reshape(n, kvh, hd)
+        v = lin(x, lp + "self_attn.v_proj").reshape(n, kvh, hd)
+        q = ops.norm_rope(q, W[p + lp + "self_attn.q_norm.weight"], eps, tables[kind], pos)
+        k = ops.norm_rope(k, W[p + lp + "self_attn.k_norm.weight"], eps, tables[kind], pos)
+        v = ops.norm_rope(v, None, eps)
+        window = tc["sliding_window"] if kind == "sliding_attention" else -1
+        a = ops.attention(q, k, v, cu, causal=False, window=window, scale=1.0)
+        a = lin(a.reshape(n, heads * hd), lp + "self_attn.o_proj")
+        h = h + opro.rms_norm(a, W[p + lp + "post_attention_layernorm.weight"], eps)
+        m = opro.rms_norm(h, W[p + lp + "pre_feedforward_layernorm.weight"], eps)
+        m = lin(gelu_tanh(lin(m, lp + "mlp.gate_proj")) * lin(m, lp + "mlp.up_proj"), lp + "mlp.down_proj")
+        h = h + opro.rms_norm(m, W[p + lp + "post_feedforward_layernorm.weight"], eps)
+        g = gelu_tanh(lin(h, lp + "ple_block.per_layer_input_gate")) * per_layer[:, i, :]
+        h = h + opro.rms_norm(lin(g, lp + "ple_block.per_layer_projection"),
+                              W[p + lp + "ple_block.post_per_layer_input_norm.weight"], eps)
+        h = h * W[p + lp + "layer_scalar"][0]
+    h = opro.rms_norm(h, W[p + "norm.weight"], eps)
+    pooled = ops.mean_pool(h, cu)
+    return ops.l2(lin(pooled, "embedding_projection")), lens
