@@ -111,7 +111,28 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
     }
   }
 
-  if (p.rotary_dim > 0) {
+  if (p.rotary_dim == 8 && p.sections == 1) {
+    // Both halves of the rotated section sit in chunk 0: pairs (e, e + 4)
+    // rotate inside the lane, by table column e (4 columns).
+    if (j == 0 && valid) {
+      const int32_t pos = p.rows[tok];
+      if (pos < 0 || pos >= p.table_rows) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = __builtin_nanf("");
+      } else {
+        const f32x4 c = *reinterpret_cast<const f32x4*>(p.cos + (int64_t)pos * 4);
+        const f32x4 s = *reinterpret_cast<const f32x4*>(p.sin + (int64_t)pos * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float ce = c[e], se = s[e];
+          if (p.round_tables) { ce = round_bf16(ce); se = round_bf16(se); }
+          const float a = v[e], b = v[e + 4];
+          v[e] = a * ce - b * se;
+          v[e + 4] = b * ce + a * se;
+        }
+      }
+    }
+  } else if (p.rotary_dim > 0) {
     // Geometry of the half-split this lane belongs to.
     int sec_lanes, sec0;  // lanes per rotated section, first lane of it
     if (p.sections == 2) {
@@ -176,8 +197,8 @@ extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, voi
   if (d->rotary_dim < 0) return fail(INL_E_INVALID, "norm_rope: rotary_dim < 0");
   if (d->rotary_dim > 0) {
     if (d->sections == 1) {
-      if (d->rotary_dim > hd || d->rotary_dim % 16)
-        return fail(INL_E_UNSUPPORTED, "norm_rope: rotary_dim must be a multiple of 16, <= head_dim");
+      if (d->rotary_dim > hd || (d->rotary_dim % 16 && d->rotary_dim != 8))
+        return fail(INL_E_UNSUPPORTED, "norm_rope: rotary_dim must be 8 or a multiple of 16, <= head_dim");
     } else if (d->sections == 2) {
       if (d->rotary_dim != hd || hd % 32)
         return fail(INL_E_UNSUPPORTED, "norm_rope: axial rope needs rotary_dim == head_dim, a multiple of 32");

@@ -159,7 +159,7 @@ typedef struct inl_norm_rope_desc {
   int32_t out_dtype;              /* y dtype */
   int32_t norm;                   /* 1 = apply the RMSNorm */
   float eps;
-  int32_t rotary_dim;             /* 0 = no rope; sections 1: multiple of 16 <= head_dim */
+  int32_t rotary_dim;             /* 0 = no rope; sections 1: 8 or a multiple of 16 <= head_dim */
   int32_t sections;               /* 1 = half-split, 2 = axial */
   int32_t table_rows;
   int32_t round_tables;

@@ -77,6 +77,8 @@ CASES = [
     ("modernbert_rope_only", 12, 64, False, False, 160000.0, 64, 0),
     ("qwen35_partial", 16, 256, True, True, 1e7, 64, 1),
     ("tiny_head_dim16", 4, 16, True, True, 1e4, 16, 0),
+    ("tiny_head_dim8", 4, 8, False, False, 1e4, 8, 0),
+    ("partial_rotary8", 4, 32, True, True, 1e4, 8, 0),
 ]
 
 

@@ -81,3 +81,60 @@ def test_gemma2_tiny_hip_matches_golden(gemma2, cuda, inl):
     import torch
     worst = _check_gemma2(gemma2, te.HipOps(inl, torch, cuda))
     print(f"tiny EmbeddingGemma2 HIP: worst max-abs {worst:.3g}")
+
+
+# ---------------------------------------------------------------------------
+# Tiny SPLADE (ModernBERT MLM, 5 layers, 4 heads of 8, local radius 4)
+# ---------------------------------------------------------------------------
+
+SPLADE_TOL = 1e-4   # modernbert.rs:1045,1054 (exact index sets, weights to 1e-4)
+
+
+@pytest.fixture(scope="module")
+def splade():
+    return te.load_fixture("tiny_splade")
+
+
+def _check_splade(fx, ops, tol=SPLADE_TOL):
+    """Every case (document / query prefix, max_length 64 / 12), batched and
+    alone: the active-term set exactly, the weights within ``tol``."""
+    worst = 0.0
+    for case in fx[2]["cases"]:
+        label = f"{case['kind']}/{case['max_length']}"
+        rows = [r["ids"] for r in case["batched"]]
+        runs = [("batched", case["batched"], te.modernbert_splade(fx, rows, ops))]
+        runs.append(("alone", case["alone"], [te.modernbert_splade(fx, [r["ids"]], ops)[0]
+                                                for r in case["alone"]]))
+        for mode, want, got in runs:
+            for i, (row, (idx, val)) in enumerate(zip(want, got)):
+                assert idx.tolist() == row["indices"], f"{label} {mode}[{i}]: active terms differ"
+                err = float(np.abs(val - np.asarray(row["values"], dtype=np.float32)).max())
+                assert err <= tol, f"{label} {mode}[{i}]: weight error {err:.3g}"
+                worst = max(worst, err)
+    return worst
+
+
+def test_splade_tiny_oracle_matches_golden(splade):
+    worst = _check_splade(splade, te.OracleOps())
+    print(f"tiny SPLADE oracle: worst weight error {worst:.3g}")
+
+
+@pytest.mark.parametrize("kind", ["window+1", "window-1", "causal"])
+def test_splade_tiny_golden_rejects_mask_mistakes(splade, kind):
+    """An off-by-one local radius or a causal mask changes the 43-token
+    row's active terms or moves its weights past the bound."""
+    case = splade[2]["cases"][0]
+    row = case["batched"][1]
+    idx, val = te.modernbert_splade(splade, [row["ids"]], _Planted(kind))[0]
+    same = idx.tolist() == row["indices"]
+    assert not same or np.abs(val - np.asarray(row["values"])).max() > 10 * SPLADE_TOL
+
+
+@pytest.mark.gpu
+def test_splade_tiny_hip_matches_golden(splade, cuda, inl):
+    """The same forward with attention (f32, head dim 8, local and global),
+    RoPE and the SPLADE epilogue (row max, finish, canonical fold) on the
+    GPU."""
+    import torch
+    worst = _check_splade(splade, te.HipOps(inl, torch, cuda))
+    print(f"tiny SPLADE HIP: worst weight error {worst:.3g}")

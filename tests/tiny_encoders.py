@@ -60,11 +60,19 @@ class OracleOps:
             y = opro.rope(y, cos[pos][:, None, :].astype(np.float64), sin[pos][:, None, :].astype(np.float64))
         return y
 
+    def rope(self, x, table, pos):
+        cos, sin = table
+        return opro.rope(x.astype(np.float64), cos[pos][:, None, :].astype(np.float64),
+                         sin[pos][:, None, :].astype(np.float64))
+
     def attention(self, q, k, v, cu, *, causal, window, scale):
         return oa.varlen_attention(q, k, v, cu, causal=causal, window=window, scale=scale)
 
     def mean_pool(self, h, cu):
         return opool.mean_pool(h, cu)
+
+    def splade(self, logits, ends, bias, shift, masked, canonical):
+        return opool.splade_pool(logits, ends, bias, shift, masked, canonical)
 
     def l2(self, x):
         return opool.l2_normalize(x)
@@ -90,6 +98,20 @@ class HipOps:
                       cos=self._t(cos), sin=self._t(sin))
         y = self.inl.norm_rope(self._t(x), weight=w, eps=eps, **kw)
         return y.cpu().numpy().astype(np.float64)
+
+    def rope(self, x, table, pos):
+        cos, sin = table
+        rows = self.torch.from_numpy(np.ascontiguousarray(pos, dtype=np.int32)).to(self.dev)
+        y = self.inl.norm_rope(self._t(x), rows, self._t(cos), self._t(sin), norm=False)
+        return y.cpu().numpy().astype(np.float64)
+
+    def splade(self, logits, ends, bias, shift, masked, canonical):
+        offs = np.concatenate([[0], np.asarray(ends)]).astype(np.int32)
+        out = self.inl.pool_splade(
+            self._t(logits), self.torch.from_numpy(offs).to(self.dev), bias=self._t(bias), shift=shift,
+            masked_ids=masked,
+            canonical=self.torch.from_numpy(np.asarray(canonical, dtype=np.int32)).to(self.dev))
+        return out.cpu().numpy()
 
     def attention(self, q, k, v, cu, *, causal, window, scale):
         o = self.inl.varlen_attention(self._t(q), self._t(k), self._t(v), [int(c) for c in cu],
@@ -175,3 +197,71 @@ def gemma2_embed(fixture, texts, max_length: int, ops):
     h = opro.rms_norm(h, W[p + "norm.weight"], eps)
     pooled = ops.mean_pool(h, cu)
     return ops.l2(lin(pooled, "embedding_projection")), lens
+
+
+# ---------------------------------------------------------------------------
+# ModernBERT MLM + SPLADE pooling (crates/inl-sparse/src/modernbert.rs)
+# ---------------------------------------------------------------------------
+
+def layer_norm(x, weight, eps):
+    """candle ``LayerNorm::new_no_bias``: ``(x - mean) / sqrt(var + eps) * w``."""
+    mu = x.mean(axis=-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(axis=-1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps) * weight
+
+
+def gelu_erf(x):
+    """candle ``Tensor::gelu_erf``."""
+    from scipy.special import erf
+    return 0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))
+
+
+def modernbert_splade(fixture, rows, ops):
+    """Sparse SPLADE vectors ``[(indices, values)]`` of the pre-tokenized
+    ``rows``, following modernbert.rs:621-655 (embedding norm, layers with
+    the identity pre-attention norm on layer 0, global layers every
+    ``global_attn_every_n_layers`` with the full-attention RoPE base, local
+    layers masked to ``|q - k| <= local_attention / 2``, scale
+    ``head_dim^-0.5``, GeGLU MLP with erf gelu), the MLM head and tied decoder
+    of :657-662 on the speaking positions (:703-716), and the pooling of
+    :806-907 (row max, ``ln(1 + relu(max + bias - shift))`` with the masked
+    vocabulary, canonical fold), then ``SparseVector::from_pairs``
+    (crates/inl-sparse/src/lib.rs:51-62)."""
+    cfg, W, _, fdir = fixture
+    pool = json.loads((fdir / "pooling_config.json").read_text())
+    lens = [len(r) for r in rows]
+    cu = oa.cu_from_lengths(lens)
+    flat = np.concatenate([np.asarray(r, dtype=np.int64) for r in rows])
+    pos = _positions(lens)
+    hs, heads, eps = cfg["hidden_size"], cfg["num_attention_heads"], cfg.get("norm_eps", 1e-5)
+    hd, inter = hs // heads, cfg["intermediate_size"]
+    n = flat.shape[0]
+    emb = W["model.embeddings.tok_embeddings.weight"]
+    rope = cfg["rope_parameters"]
+    positions = max(lens)
+    tables = {True: opro.rope_table(hd, rope["full_attention"]["rope_theta"], positions),
+              False: opro.rope_table(hd, rope["sliding_attention"]["rope_theta"], positions)}
+    h = layer_norm(emb[flat], W["model.embeddings.norm.weight"], eps)
+    for i in range(cfg["num_hidden_layers"]):
+        lp = f"model.layers.{i}."
+        glob = i % cfg["global_attn_every_n_layers"] == 0
+        x = h if i == 0 else layer_norm(h, W[lp + "attn_norm.weight"], eps)
+        wqkv = W[lp + "attn.Wqkv.weight"]
+        q = (x @ wqkv[:hs].T).reshape(n, heads, hd)
+        k = (x @ wqkv[hs:2 * hs].T).reshape(n, heads, hd)
+        v = (x @ wqkv[2 * hs:].T).reshape(n, heads, hd)
+        q = ops.rope(q, tables[glob], pos)
+        k = ops.rope(k, tables[glob], pos)
+        window = -1 if glob else cfg["local_attention"] // 2
+        a = ops.attention(q, k, v, cu, causal=False, window=window, scale=hd ** -0.5)
+        h = h + a.reshape(n, hs) @ W[lp + "attn.Wo.weight"].T
+        m = layer_norm(h, W[lp + "mlp_norm.weight"], eps)
+        wi = W[lp + "mlp.Wi.weight"]
+        h = h + (gelu_erf(m @ wi[:inter].T) * (m @ wi[inter:].T)) @ W[lp + "mlp.Wo.weight"].T
+    h = layer_norm(h, W["model.final_norm.weight"], eps)
+    index, ends = opool.speakers(rows, pool["prefix_token_ids"])
+    head = layer_norm(gelu_erf(h[index] @ W["head.dense.weight"].T), W["head.norm.weight"], eps)
+    logits = (head @ emb.T).astype(np.float32)
+    dense = ops.splade(logits, ends, W["decoder.bias"].astype(np.float32), pool["logit_shift"],
+                       pool["masked_vocab_ids"], pool["canonical_ids"])
+    return [opool.sparse_from_pairs(row) for row in dense]
