@@ -221,11 +221,12 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     for (int i = 0; i < KST; ++i)
       qreg[i] = __builtin_amdgcn_raw_buffer_load_b128(qrs, qrow_b + (2 * i + hf) * 16, 0, 0);
   };
-  // Q^T operand of unit u, loaded while the current unit's state stays in
-  // place (its last softmax still needs it). Issued from inline asm like the
-  // K/V loads, so the compiler tracks none of the loop's global loads; the
-  // wait at the end of the softmax phase takes qreg as operands, so no use
-  // of qreg can move ahead of it.
+  // Q^T operand of unit u, loaded into qn one stream step before the step
+  // that switches to u: it then has a whole MFMA phase and softmax phase to
+  // land, like the K/V tiles. Issued from inline asm like the K/V loads, so
+  // the compiler tracks none of the loop's global loads; the wait at the end
+  // of the softmax phase takes qn as operands, so no use of qn can move ahead
+  // of it.
   auto q_addr = [&](int u, i32x4& rs, uint32_t& qa) __attribute__((always_inline)) {
     int sg, tn, q0, lo, hi, hg;
     unit(u, sg, tn, q0, lo, hi, hg);
@@ -234,6 +235,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     rs = pp_rsrc_words(p.q + ((int64_t)sg * p.q_stride + (int64_t)hd * D) * 2, (uint32_t)tn * qst_b);
     qa = (uint32_t)(q0 + (wave % p.rb) * 32 + lq) * qst_b + hf * 16;
   };
+  u32x4 qn[KST];   // the next unit's Q^T, in flight until the cursor reaches it
   auto load_q_of = [&](int u) __attribute__((always_inline)) {
     i32x4 rs;
     uint32_t qa;
@@ -241,7 +243,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < KST; ++i)
       asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
-                   : "=v"(qreg[i]) : "v"(qa), "s"(rs), "n"(32 * i) : "memory");
+                   : "=v"(qn[i]) : "v"(qa), "s"(rs), "n"(32 * i) : "memory");
   };
 
 
@@ -256,6 +258,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   dma_tile(S::TILE);
   lds_barrier();
+  if (hi_t - lo_t == 1 && nu > 1) load_q_of(1);
 
   f32x16 oacc[NDB];
 #pragma unroll
@@ -442,17 +445,21 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       if (!LAST && ks + 2 >= PKS) kfrag(sK, ks + 2 - PKS, kr[ks + 2 - PKS]);
       __builtin_amdgcn_sched_barrier(0);
     }
+    // A finished unit's output goes out right after its last PV, so that the
+    // stores have this phase and the next softmax phase to complete before the
+    // wait at that phase's end (which counts stores as well as loads). Staged
+    // through the K half of stage st - 1: both groups' QK^T of that tile are
+    // done, and its next load is issued after this tile's MFMA phases.
+    if (__builtin_expect(fin, 0)) {
+      store_out(lds0 + ((st + (S::STAGES - 1) * S::TILE) & (S::STAGES * S::TILE - 1)) + (wave & 3) * 4096);
+      fin = false;
+    }
+    __builtin_amdgcn_sched_barrier(0);
     // The V slice to convert is read behind the first K fragments and written
     // back during QK^T, so that waiting for it never holds up an MFMA.
     if (!LAST) conv_read(sVc, w);
     __builtin_amdgcn_sched_barrier(0);
     if (!LAST) qk_body(sK, kr, [&]() __attribute__((always_inline)) { conv_write(sVc, w); });
-    if (__builtin_expect(fin, 0)) {
-      // The K half of stage st - 1: both groups' QK^T of that tile are done,
-      // and its next load is issued after this tile's MFMA phases.
-      store_out(lds0 + ((st + (S::STAGES - 1) * S::TILE) & (S::STAGES * S::TILE - 1)) + (wave & 3) * 4096);
-      fin = false;
-    }
   };
 
   // P (fp16) and its per-lane sum over this tile, with reference max `base`.
@@ -519,10 +526,6 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   int t = lo_t;
   bool done = false;
   auto vphase = [&](uint32_t dst) __attribute__((always_inline)) {
-    // On a unit's last tile the next unit's Q goes out first: the loads
-    // issued after it (this phase's K/V) then need not land before the
-    // wait at the end of the phase covers the Q loads.
-    if (__builtin_expect(t + 1 == hi_t && cu + 1 < nu, 0)) load_q_of(cu + 1);
     dma_part(0, dst);
     __builtin_amdgcn_sched_barrier(0);
     if (__builtin_expect((uint32_t)(t - f_lo) >= (uint32_t)f_n, 0)) apply_mask(t);
@@ -564,12 +567,14 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     for (int i = PKS + 1; i < DMA_PARTS; ++i) dma_part(i, dst);
     __builtin_amdgcn_sched_barrier(0);
     dma_advance();
+    bool next_q = false;
     if (__builtin_expect(t + 1 == hi_t, 0)) {
       capture_out();
       fin = true;
       if (cu + 1 < nu) {
         set_unit(++cu);
         t = lo_t - 1;
+        next_q = true;
       } else {
         done = true;
       }
@@ -577,13 +582,20 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     ++t;
     // Loads retire from vmcnt in issue order, stores independently of
     // them: with at most 2 * KPW ops in flight, every load older than this
-    // phase's K/V loads (the Q loads among them) is done, whatever the
+    // phase's K/V loads (qn's loads among them) is done, whatever the
     // stores do.
     static_assert(KST == 8, "the wait below names eight Q registers");
     asm volatile("s_waitcnt vmcnt(%8)"
-                 : "+v"(qreg[0]), "+v"(qreg[1]), "+v"(qreg[2]), "+v"(qreg[3]), "+v"(qreg[4]), "+v"(qreg[5]),
-                   "+v"(qreg[6]), "+v"(qreg[7])
+                 : "+v"(qn[0]), "+v"(qn[1]), "+v"(qn[2]), "+v"(qn[3]), "+v"(qn[4]), "+v"(qn[5]),
+                   "+v"(qn[6]), "+v"(qn[7])
                  : "n"(2 * S::KPW) : "memory");
+    if (__builtin_expect(next_q, 0)) {
+#pragma unroll
+      for (int i = 0; i < KST; ++i) qreg[i] = qn[i];
+    }
+    // The next step processes the current unit's last tile: the unit after
+    // it gets its Q now, behind this phase's K/V loads.
+    if (__builtin_expect(t + 1 == hi_t && cu + 1 < nu, 0)) load_q_of(cu + 1);
   };
 
   // ---- the stream, in barrier-separated half-slots ----
