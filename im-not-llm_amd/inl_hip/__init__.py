@@ -294,6 +294,31 @@ def attention_flops(lengths, h_q, head_dim, causal, window=-1) -> int:
                     hi = min(hi, qi + 1)
                 total += hi - max(0, qi - w)
     return 4 * h_q * head_dim * total
+_plan_packed = _sig("inl_plan_packed_batches", ctypes.c_int, c_void_p, c_i64, c_i64, c_i64,
+                    c_void_p, ctypes.POINTER(c_i64))
+
+
+# ---------------------------------------------------------------------------
+# Packed batch planner
+# ---------------------------------------------------------------------------
+
+def plan_packed_batches(lengths, max_items: int, max_tokens: int):
+    """Consecutive batches (``range`` objects over the inputs, in order) of at
+    most ``max_items`` inputs and ``max_tokens`` real tokens; the packed
+    counterpart of the reference's padded ``plan_batches``
+    (crates/inl-sparse/src/native.rs:557-582, crates/inl-text/src/native.rs:
+    698-735). An input over ``max_tokens`` forms a batch by itself."""
+    import numpy as np
+    ln = np.ascontiguousarray(lengths, dtype=np.int32)
+    ends = np.empty(max(len(ln), 1), dtype=np.int64)
+    nb = c_i64()
+    _check(_plan_packed(ln.ctypes.data, len(ln), int(max_items), int(max_tokens), ends.ctypes.data,
+                        ctypes.byref(nb)))
+    out, start = [], 0
+    for e in ends[:nb.value]:
+        out.append(range(start, int(e)))
+        start = int(e)
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -234,6 +234,26 @@ int inl_pool_splade_fwd(int32_t rows, const int32_t* offs, int32_t vocab,
                         void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Packed batch planner (host). Replaces the padded planners of the text,
+ * sparse, late and vision engines (crates/inl-text/src/native.rs:698-735,
+ * crates/inl-sparse/src/native.rs:557-582, crates/inl-late/src/native.rs:
+ * 694-719, crates/inl-vision/src/engine.rs:782-798), which split inputs in
+ * order into consecutive batches of at most `batch_size` inputs and at most
+ * `max_batch_tokens` PADDED tokens (inputs x longest), plus, for text, an
+ * attention-score budget. Packed into one cu_seqlens row set, a batch costs
+ * its REAL tokens: this planner caps sum(lengths) instead, and the fused
+ * attention keeps no score matrix, so no score budget applies.
+ *   lengths:   host [n] token counts, in the caller's order (>= 0; a length of
+ *              0 counts as 1 token, as the reference's `length.max(1)`);
+ *   batch_end: host [n], receives each batch's exclusive end index;
+ *   n_batches: receives the number of batches (0 for n == 0).
+ * A single input over `max_tokens` forms a batch by itself, as in the
+ * reference. The split is greedy, and greedy is optimal here (fewest
+ * batches) because a feasible batch stays feasible without its first input. */
+int inl_plan_packed_batches(const int32_t* lengths, int64_t n, int64_t max_items, int64_t max_tokens,
+                            int64_t* batch_end, int64_t* n_batches);
+
+/* ------------------------------------------------------------------------ */
 const char* inl_last_error(void);
 int32_t inl_abi_version(void);
 

@@ -13,6 +13,8 @@ implementation performs on the encoder attention hot path:
   Matryoshka truncation and the sparse active-term set;
 * ``tiny_models`` - the tiny EmbeddingGemma 2 and ModernBERT-SPLADE encoders
   of the reference's golden fixtures, used to pin the forms above in situ;
+* ``planner``    - the reference's padded batch planner, its packed
+  counterpart and a brute-force optimum for small inputs;
 * ``cref``       - a ctypes loader for ``attn_ref.c``, the multi-threaded f32
   C restatement used as the CPU baseline.
 
