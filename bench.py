@@ -207,7 +207,7 @@ def main():
     bn = plans[0].info()["block_n"]
     kernel = (f"attn_pp_kernel<{d}, {bn}>" if d == 128
               else f"attn_wide_kernel<{d}, {bn}>" if d == 256
-              else f"attn_pp64_kernel<{d}, {bn}>" if d == 64 and hq == hkv and hq % 2 == 0
+              else f"attn_pp64_kernel<{bn}>" if d == 64 and hq == hkv and hq % 2 == 0
               else f"attn_bf16_kernel<{d}, {bn}, 4>" if d == 64
               else f"attn_fwd_kernel<bf16, {d}, {bn}>")
     n_launch = len(batches)

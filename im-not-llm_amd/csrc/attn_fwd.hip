@@ -572,7 +572,8 @@ struct CostedItem {
 
 // Persistent schedule: every (item, head group) unit goes to the workgroup
 // with the least work so far (longest units first, LPT). A workgroup costs
-// its tiles plus about one tile of per-unit overhead (Q load, output store).
+// its tiles plus the per-unit overhead (Q load, output store, first-tile
+// set-up), measured at about 2.3 tiles of head_dim 128 work per unit.
 // Workgroups are dispatched to the 8 XCDs round-robin (b % 8), and each XCD
 // has its own L2; when the head groups split evenly over the XCDs, units of
 // head group h run only on workgroups b with b % 8 == h % 8, so the K/V rows
@@ -599,7 +600,7 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, Schedule* s) {
       Load top = h.top();
       h.pop();
       lists[top.second].push_back((int64_t)i * n_hg + hg);
-      if ((int)lists[top.second].size() < PP_MAX_UNITS) h.push(Load(top.first + 4 * items[i].cost + 3, top.second));
+      if ((int)lists[top.second].size() < PP_MAX_UNITS) h.push(Load(top.first + 4 * items[i].cost + 9, top.second));
     }
   s->items.reserve(U);
   s->unit_hg.reserve(U);
