@@ -44,6 +44,7 @@
 #include <mutex>
 #include <new>
 #include <queue>
+#include <unordered_map>
 #include <vector>
 
 #include "attn_kernels.hpp"
@@ -570,7 +571,8 @@ struct CostedItem {
   int cost;  // key tiles
 };
 
-// Persistent schedule: every (item, head group) unit goes to the workgroup
+// Persistent schedule (`gpk`: head groups per KV head, consecutive in hg):
+// every (item, head group) unit goes to the workgroup
 // with the least work so far (longest units first, LPT). A workgroup costs
 // its tiles plus the per-unit overhead (Q load, output store, first-tile
 // set-up), measured at about 2.3 tiles of head_dim 128 work per unit.
@@ -578,7 +580,7 @@ struct CostedItem {
 // has its own L2; when the head groups split evenly over the XCDs, units of
 // head group h run only on workgroups b with b % 8 == h % 8, so the K/V rows
 // a head group reads are fetched into one L2.
-void assign_units(const std::vector<CostedItem>& items, int n_hg, Schedule* s) {
+void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Schedule* s) {
   const int64_t U = (int64_t)items.size() * n_hg;
   s->items.clear();
   s->unit_hg.clear();
@@ -586,25 +588,88 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, Schedule* s) {
   if (U == 0) return;
   const int n_cu = device_cus();
   const bool affinity = n_hg % 8 == 0;
-  const int classes = affinity ? 8 : 1;
   int64_t n_wg = std::min<int64_t>(n_cu, U);
   n_wg = std::max<int64_t>(n_wg, (U + PP_MAX_UNITS - 1) / PP_MAX_UNITS);
-  n_wg = (n_wg + classes - 1) / classes * classes;
+  n_wg = (n_wg + 7) / 8 * 8;
+  // Stream affinity: without head-group affinity, each (text, KV head)
+  // stream goes to one XCD class (streams longest-first to the class with
+  // the least work), so the q-blocks that re-read a stream's K/V rows share
+  // one L2. Used when there are enough streams to balance the 8 classes and
+  // no class outgrows its workgroups' unit tables.
+  const int n_kv = n_hg / gpk;
+  std::vector<int> stream_class;
+  bool streams = false;
+  if (!affinity && n_wg >= 8 && (int64_t)items.size() * n_kv >= 32) {
+    std::vector<int64_t> seg_cost;   // per (text, KV head); texts numbered in first-seen order
+    std::vector<int> text_of(items.size());
+    std::unordered_map<int, int> text_id;   // text start row -> text number
+    for (size_t i = 0; i < items.size(); ++i)
+      text_of[i] = text_id.emplace(items[i].it.x, (int)text_id.size()).first->second;
+    const int64_t n_streams = (int64_t)text_id.size() * n_kv;
+    if (n_streams >= 32) {
+      seg_cost.assign(n_streams, 0);
+      std::vector<int64_t> seg_units(n_streams, 0);
+      for (size_t i = 0; i < items.size(); ++i)
+        for (int kv = 0; kv < n_kv; ++kv) {
+          seg_cost[(int64_t)text_of[i] * n_kv + kv] += (int64_t)gpk * (4 * items[i].cost + 9);
+          seg_units[(int64_t)text_of[i] * n_kv + kv] += gpk;
+        }
+      std::vector<int64_t> order(n_streams);
+      for (int64_t k = 0; k < n_streams; ++k) order[k] = k;
+      std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return seg_cost[a] > seg_cost[b]; });
+      std::vector<int> cls(n_streams);
+      std::vector<int64_t> cls_units(8, 0);
+      std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>, std::greater<std::pair<int64_t, int>>> ch;
+      for (int c = 0; c < 8; ++c) ch.push({0, c});
+      for (int64_t k : order) {
+        auto top = ch.top();
+        ch.pop();
+        cls[k] = top.second;
+        cls_units[top.second] += seg_units[k];
+        ch.push({top.first + seg_cost[k], top.second});
+      }
+      streams = *std::max_element(cls_units.begin(), cls_units.end()) <= (n_wg / 8) * (int64_t)PP_MAX_UNITS;
+      if (streams) {
+        stream_class.resize(items.size() * n_kv);
+        for (size_t i = 0; i < items.size(); ++i)
+          for (int kv = 0; kv < n_kv; ++kv) stream_class[i * n_kv + kv] = cls[(int64_t)text_of[i] * n_kv + kv];
+      }
+    }
+  }
+  const int classes = affinity || streams ? 8 : 1;
   std::vector<std::vector<int64_t>> lists(n_wg);  // unit = item * n_hg + hg
   typedef std::pair<int64_t, int64_t> Load;       // (cost so far, workgroup)
   std::vector<std::priority_queue<Load, std::vector<Load>, std::greater<Load>>> heaps(classes);
   for (int64_t b = 0; b < n_wg; ++b) heaps[b % classes].push(Load(0, b));
-  for (size_t i = 0; i < items.size(); ++i)
-    for (int hg = 0; hg < n_hg; ++hg) {
-      auto& h = heaps[hg % classes];
-      Load top = h.top();
-      h.pop();
-      lists[top.second].push_back((int64_t)i * n_hg + hg);
-      if ((int)lists[top.second].size() < PP_MAX_UNITS) h.push(Load(top.first + 4 * items[i].cost + 9, top.second));
-    }
+  auto place = [&](size_t i, int hg) {
+    auto& h = heaps[streams ? stream_class[i * n_kv + hg / gpk] : hg % classes];
+    Load top = h.top();
+    h.pop();
+    lists[top.second].push_back((int64_t)i * n_hg + hg);
+    if ((int)lists[top.second].size() < PP_MAX_UNITS) h.push(Load(top.first + 4 * items[i].cost + 9, top.second));
+  };
+  // Longest first; among units of equal cost, KV head major, then item, then
+  // the head groups that share the KV head, so that the consecutive units
+  // that land on one XCD read the same K/V rows.
+  for (size_t i0 = 0; i0 < items.size();) {
+    size_t i1 = i0 + 1;
+    while (i1 < items.size() && items[i1].cost == items[i0].cost) ++i1;
+    for (int kv = 0; kv < n_hg / gpk; ++kv)
+      for (size_t i = i0; i < i1; ++i)
+        for (int g = 0; g < gpk; ++g) place(i, kv * gpk + g);
+    i0 = i1;
+  }
   s->items.reserve(U);
   s->unit_hg.reserve(U);
-  for (int64_t b = 0; b < n_wg; ++b) {
+  // Without head-group affinity, equal-cost units (the q-blocks of one text,
+  // and the head groups of one item, in order) go round-robin to logical
+  // workgroups 0, 1, 2, ...; workgroup b = 8 j + x runs logical list
+  // x * (n_wg / 8) + j, so each run of n_wg / 8 consecutive lists shares one
+  // XCD and its L2 holds the K/V rows that neighbouring q-blocks re-read.
+  const bool spread = classes == 1 && n_wg % 8 == 0;
+  const int64_t per_xcd = n_wg / 8;
+  for (int64_t pb = 0; pb < n_wg; ++pb) {
+    const int64_t b = spread ? (pb % 8) * per_xcd + pb / 8 : pb;
     for (int64_t u : lists[b]) {
       s->items.push_back(items[u / n_hg].it);
       s->unit_hg.push_back((int32_t)(u % n_hg));
@@ -657,7 +722,7 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
   if (s->cfg.persistent) {
     if ((int64_t)tmp.size() * s->n_hg > INT32_MAX)
       return fail(INL_E_UNSUPPORTED, "attention: too many tiles for one launch");
-    assign_units(tmp, s->n_hg, s);
+    assign_units(tmp, s->n_hg, s->cfg.head_pairs ? 1 : group / s->hpw, s);
     return INL_OK;
   }
   s->items.resize(tmp.size());
