@@ -76,7 +76,26 @@ def build(verbose: bool = False) -> Path:
         if rc != 0:
             raise RuntimeError(f"hipcc link failed ({rc}):\n{err}")
     os.replace(tmp, OUT)
+    _build_test_shims()
     return OUT
+
+
+# Test shims under tests/cpp/: host C++ that drives the library's C++
+# interface (include/inl_attention.hpp) from pytest through ctypes. Built
+# here, beside the library, so that no test compiles anything.
+TEST_CPP = PKG.parent / "tests" / "cpp"
+
+
+def _build_test_shims():
+    if not TEST_CPP.is_dir():
+        return
+    for src in sorted(TEST_CPP.glob("*.cpp")):
+        out = TEST_CPP / f"lib{src.stem}.so"
+        rel = os.path.relpath(OUT.parent, TEST_CPP)
+        rc, err = _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", f"-I{INCLUDE}", str(src),
+                        f"-L{OUT.parent}", "-linl_hip", f"-Wl,-rpath,$ORIGIN/{rel}", "-o", str(out)])
+        if rc != 0:
+            raise RuntimeError(f"hipcc failed on {src.name} ({rc}):\n{err}")
 
 
 if __name__ == "__main__":
