@@ -54,7 +54,7 @@ class AttentionBackend {
   /* attention.rs:73-89 */
   static AttentionBackend resolve(AttentionRequest request, DeviceKind device, int32_t dtype, int32_t head_dim);
   /* attention.rs:114-123 */
-  size_t score_rows(size_t padded) const { return (void)padded, 0; }
+  size_t score_rows(size_t /*padded*/) const { return 0; }
   Kind kind() const { return kind_; }
 
  private:
@@ -78,7 +78,9 @@ struct MutTensor4 {
 };
 
 /* The padding of one forward pass over a [B, T] batch, and the attention
- * form of the model that runs it. */
+ * form of the model that runs it. It caches the device plan of its last
+ * attend, so one thread uses a mask at a time (the reference runs a forward
+ * under a per-model mutex, crates/inl-text/src/native.rs:580-583). */
 class BatchMask {
  public:
   /* attention.rs:139-153: Qwen3, causal, left padding pad_lens[b] per row
