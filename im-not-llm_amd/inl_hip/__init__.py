@@ -23,6 +23,15 @@ if not _LIB_PATH.exists():
         f"{_LIB_PATH} is not built; run `python im-not-llm_amd/build.py` "
         "(the HIP path has no fallback)")
 
+# torch ships its own HIP runtime with the same soname (libamdhip64.so.7).
+# Loading torch first makes this library bind to that runtime; loaded the
+# other way round the process holds two HIP runtimes, and the second one to
+# open the device finds none.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 _lib = ctypes.CDLL(str(_LIB_PATH))
 
 INL_F32 = 0
