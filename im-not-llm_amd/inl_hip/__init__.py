@@ -388,6 +388,8 @@ def norm_rope(x, rows=None, cos=None, sin=None, *, weight=None, eps=1e-6, norm=T
 
 def pool_last(hidden, cu, *, weight=None, eps=1e-6, round_norm=False, stream=None):
     import torch
+    if weight is not None and weight.dtype != hidden.dtype:
+        raise ValueError(f"pool_last: weight dtype {weight.dtype} must match hidden dtype {hidden.dtype}")
     n_texts = cu.numel() - 1
     out = torch.empty((n_texts, hidden.shape[1]), dtype=torch.float32, device=hidden.device)
     _check(_pool_last(n_texts, cu.data_ptr(), hidden.shape[1], hidden.stride(0),
