@@ -597,15 +597,16 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
   // one L2. Used when there are enough streams to balance the 8 classes and
   // no class outgrows its workgroups' unit tables.
   const int n_kv = n_hg / gpk;
+  std::vector<int> text_of(items.size());
+  std::unordered_map<int, int> text_id;   // text start row -> text number, in first-seen order
+  for (size_t i = 0; i < items.size(); ++i)
+    text_of[i] = text_id.emplace(items[i].it.x, (int)text_id.size()).first->second;
+  const int n_texts = (int)text_id.size();
   std::vector<int> stream_class;
   bool streams = false;
   if (!affinity && n_wg >= 8 && (int64_t)items.size() * n_kv >= 32) {
-    std::vector<int64_t> seg_cost;   // per (text, KV head); texts numbered in first-seen order
-    std::vector<int> text_of(items.size());
-    std::unordered_map<int, int> text_id;   // text start row -> text number
-    for (size_t i = 0; i < items.size(); ++i)
-      text_of[i] = text_id.emplace(items[i].it.x, (int)text_id.size()).first->second;
-    const int64_t n_streams = (int64_t)text_id.size() * n_kv;
+    std::vector<int64_t> seg_cost;   // per (text, KV head)
+    const int64_t n_streams = (int64_t)n_texts * n_kv;
     if (n_streams >= 32) {
       seg_cost.assign(n_streams, 0);
       std::vector<int64_t> seg_units(n_streams, 0);
@@ -648,16 +649,41 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
     lists[top.second].push_back((int64_t)i * n_hg + hg);
     if ((int)lists[top.second].size() < PP_MAX_UNITS) h.push(Load(top.first + 4 * items[i].cost + 9, top.second));
   };
-  // Longest first; among units of equal cost, KV head major, then item, then
-  // the head groups that share the KV head, so that the consecutive units
-  // that land on one XCD read the same K/V rows.
-  for (size_t i0 = 0; i0 < items.size();) {
-    size_t i1 = i0 + 1;
-    while (i1 < items.size() && items[i1].cost == items[i0].cost) ++i1;
-    for (int kv = 0; kv < n_hg / gpk; ++kv)
-      for (size_t i = i0; i < i1; ++i)
-        for (int g = 0; g < gpk; ++g) place(i, kv * gpk + g);
-    i0 = i1;
+  // Texts in groups of about one unit per workgroup (texts by total cost,
+  // longest first), each group longest unit first. The q-blocks of a text
+  // then run at about the same time, while its K/V rows are in L2 (a plain
+  // longest-first order spreads a causal text's q-blocks over the whole
+  // launch), and within a group the longest-first order keeps the balance.
+  // Among units of equal cost: KV head major, then item, then the head
+  // groups that share the KV head, so that neighbours read the same rows.
+  std::vector<int64_t> text_cost(n_texts, 0);
+  std::vector<std::vector<size_t>> text_items(n_texts);
+  for (size_t i = 0; i < items.size(); ++i) {
+    text_cost[text_of[i]] += items[i].cost;
+    text_items[text_of[i]].push_back(i);
+  }
+  std::vector<int> text_order(n_texts);
+  for (int t = 0; t < n_texts; ++t) text_order[t] = t;
+  std::stable_sort(text_order.begin(), text_order.end(),
+                   [&](int a, int b) { return text_cost[a] > text_cost[b]; });
+  std::vector<size_t> grp;
+  for (size_t t = 0; t < text_order.size();) {
+    grp.clear();
+    int64_t units = 0;
+    while (t < text_order.size() && units < n_wg) {
+      for (size_t i : text_items[text_order[t]]) grp.push_back(i);
+      units += (int64_t)text_items[text_order[t]].size() * n_hg;
+      ++t;
+    }
+    std::stable_sort(grp.begin(), grp.end(), [&](size_t a, size_t b) { return items[a].cost > items[b].cost; });
+    for (size_t j0 = 0; j0 < grp.size();) {
+      size_t j1 = j0 + 1;
+      while (j1 < grp.size() && items[grp[j1]].cost == items[grp[j0]].cost) ++j1;
+      for (int kv = 0; kv < n_hg / gpk; ++kv)
+        for (size_t j = j0; j < j1; ++j)
+          for (int g = 0; g < gpk; ++g) place(grp[j], kv * gpk + g);
+      j0 = j1;
+    }
   }
   s->items.reserve(U);
   s->unit_hg.reserve(U);
