@@ -10,20 +10,23 @@ the attention op over all 12 batches (12 launches, one plan per batch built
 before timing, as an engine builds one per batch and reuses it for every
 layer).
 
-Prints one JSON line: tokens/s (value), attention TFLOP/s, the roofline of
-the attention kernel and the CPU baseline. The roofline divides the
-algorithmic work of one launch (FLOPs: 4 * head_dim per visible (q, k) pair
-per query head; HBM bytes: Q, K, V read once and O written once) by the
-average launch time from HIP events on the launch stream, against the
-2516.6 TFLOP/s bf16 dense MFMA peak and 8 TB/s of HBM; `bound` names the
-one with the larger floor on time, and `traffic` is the measured HBM bytes
-per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary for
-the workload. The CPU baseline is the oracle's multi-threaded f32 C
-restatement of the reference CPU flash path, timed on a bounded sample of
-the same workload.
+Prints one JSON line: attention-op tokens/s (value: tokens through one
+attention layer per second), attention TFLOP/s, the roofline of the
+attention kernel and the CPU baseline. The roofline divides the algorithmic
+work of one launch (FLOPs: 4 * head_dim per visible (q, k) pair per query
+head; HBM bytes: Q, K, V read once and O written once) by the average launch
+time from HIP events on the launch stream. `bound` is "mfma": attention is
+graded against the 2516.6 TFLOP/s bf16 dense MFMA peak, with the 8 TB/s HBM
+figure under `other`. `traffic` is the measured HBM bytes per launch from
+the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary for the workload. The
+CPU baseline is the oracle's multi-threaded f32 C restatement of the
+reference CPU flash path, timed on a bounded sample of the same workload.
 
-Other workloads (--workload): gemma_window, gemma_full, modernbert_local,
-modernbert_global, vision, pplx_causal - reported the same way.
+Other attention workloads (--workload): gemma_window, gemma_full,
+modernbert_local, modernbert_global, vision, pplx_causal, qwen3_2048,
+qwen3_2048_full - reported the same way. Op workloads (--workload norm_rope,
+pool_last, pool_mean, splade) time the prologue and epilogue kernels at
+their configurations' full sizes against the 8 TB/s HBM roofline.
 """
 from __future__ import annotations
 
@@ -126,9 +129,11 @@ def cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale, seconds):
         "unit": "tokens/s",
         "cores": cref.threads(),
         "kind": "port",
+        "cpu_model": cpu_model(),
         "sample": (f"{used} batch launches ({used / len(batches):.2f} passes over the {len(batches)} batches; "
                    f"{tokens} tokens, {flops / 1e12:.4f} TFLOP) through oracle/attn_ref.c (f32 per-text "
-                   f"online-softmax attention, OpenMP), {spent:.2f} s"),
+                   f"online-softmax attention as candle's CPU flash path, 64-key blocks, 8-wide AVX2 dot "
+                   f"products, OpenMP over (text, head, 16-row block)), {spent:.2f} s"),
         "tflops": round(flops / spent / 1e12, 4),
     }
 
@@ -144,17 +149,168 @@ def read_traffic(name: str):
     return None
 
 
-def roofline(hbm_bound, tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch):
-    """The attention kernel against its binding roofline, the other beside it."""
-    mfma = {"achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
-    hbm = {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-           "frac": round(gbs / PEAK_HBM_GBS, 4)}
-    main_, other = (hbm, mfma) if hbm_bound else (mfma, hbm)
-    return {"bound": "hbm" if hbm_bound else "mfma", **main_, "traffic": traffic,
+def cpu_model() -> str:
+    """The host CPU's model line (lscpu's "Model name" with family/model)."""
+    info = {}
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                info.setdefault(k, v)
+    except OSError:
+        return "unknown"
+    return f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, model {info.get('model', '?')})"
+
+
+def roofline(tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch):
+    """The attention kernel against the bf16 dense MFMA peak (attention is a
+    dense contraction and is graded on matrix-core use), with its HBM
+    bandwidth beside it under ``other``; ``hbm_floor_exceeds_mfma_floor``
+    says when the launch's bytes, not its flops, set the lower bound on time."""
+    mfma_floor = flop_launch / (PEAK_BF16_TFLOPS * 1e12)
+    hbm_floor = bytes_launch / (PEAK_HBM_GBS * 1e9)
+    return {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
             "kernel": kernel, "avg_launch_us": round(avg_ms * 1e3, 2),
             "algorithmic_per_launch": {"flop": flop_launch, "hbm_bytes": bytes_launch},
-            "other": {"bound": "mfma" if hbm_bound else "hbm", **other}}
+            "hbm_floor_exceeds_mfma_floor": hbm_floor > mfma_floor,
+            "other": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                      "frac": round(gbs / PEAK_HBM_GBS, 4)}}
+
+
+OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade")
+
+
+def op_workload(name, torch, inl_hip, dev):
+    """The prologue and epilogue kernels at their configurations' full sizes.
+    Returns (label, kernel, launches per step, step(evs), tokens per step,
+    algorithmic HBM bytes per step, dtype). Bytes are what the op must move:
+    its inputs read once and its outputs written once (SURVEY-style per-unit
+    figures, stated in each label)."""
+    from inl_hip import workloads as w
+    g = torch.Generator(device=dev).manual_seed(3)
+    stream = torch.cuda.current_stream()
+
+    def timed(launches):
+        def step(evs=None):
+            for i, fn in enumerate(launches):
+                if evs is not None:
+                    evs[i][0].record(stream)
+                fn()
+                if evs is not None:
+                    evs[i][1].record(stream)
+        return step
+
+    if name == "norm_rope":
+        # config 2 batches: per batch, q (16 heads, q_norm weight) and k (8 heads,
+        # k_norm weight) of a fused [T, 32, 128] bf16 QKV projection output,
+        # RMSNorm (eps 1e-6) + RoPE (theta 1e6), bf16 out
+        lens = w.qwen3_op_lengths()
+        bats = w.batches(lens, 64)
+        c, s_ = inl_hip.rope_table(128, 1e6, 2048)
+        cos, sin = torch.from_numpy(c).to(dev), torch.from_numpy(s_).to(dev)
+        launches, nbytes = [], 0
+        for b in bats:
+            cu = w.cu_seqlens(b)
+            T = cu[-1]
+            qkv = torch.randn(T, 32, 128, generator=g, device=dev).to(torch.bfloat16)
+            rows = torch.from_numpy(inl_hip.positions(cu)).to(dev)
+            wq = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+            wk = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+            qo = torch.empty(T, 16, 128, device=dev, dtype=torch.bfloat16)
+            ko = torch.empty(T, 8, 128, device=dev, dtype=torch.bfloat16)
+            launches.append(lambda qkv=qkv, rows=rows, wq=wq, qo=qo: inl_hip.norm_rope(
+                qkv[:, :16], rows, cos, sin, weight=wq, eps=1e-6, out=qo, stream=stream))
+            launches.append(lambda qkv=qkv, rows=rows, wk=wk, ko=ko: inl_hip.norm_rope(
+                qkv[:, 16:24], rows, cos, sin, weight=wk, eps=1e-6, out=ko, stream=stream))
+            # per launch: x read and y written (heads*128*2 B each per token), the
+            # positions (4 B per token), the weight, and the cos/sin rows of the
+            # batch's longest text (2 tables x 64 floats per position)
+            for heads in (16, 8):
+                nbytes += T * heads * 128 * 2 * 2 + T * 4 + 128 * 2 + max(b) * 64 * 4 * 2
+        label = (f"config2 prologue: q/k RMSNorm+RoPE (Qwen3-0.6B: 16 q / 8 k heads x 128, bf16 in/out, "
+                 f"theta 1e6) over {sum(lens)} tokens in 12 batches, 2 launches per batch")
+        return label, "norm_rope_kernel<bf16, bf16>", len(launches), timed(launches), sum(lens), nbytes, "bf16"
+    if name == "pool_last":
+        # config 2 batches: final RMSNorm of each text's last row (hidden 1024,
+        # bf16) and the f32 L2 normalisation
+        lens = w.qwen3_op_lengths()
+        bats = w.batches(lens, 64)
+        launches, nbytes = [], 0
+        wt = (1 + 0.1 * torch.randn(1024, generator=g, device=dev)).to(torch.bfloat16)
+        for b in bats:
+            cu = torch.tensor(w.cu_seqlens(b), dtype=torch.int32, device=dev)
+            h = torch.randn(int(sum(b)), 1024, generator=g, device=dev).to(torch.bfloat16)
+            launches.append(lambda h=h, cu=cu: inl_hip.pool_last(h, cu, weight=wt, eps=1e-6, stream=stream))
+            nbytes += len(b) * 1024 * 2 + 1024 * 2 + len(b) * 1024 * 4 + (len(b) + 1) * 4
+        label = ("config2 last-token epilogue: final RMSNorm + L2 of each text's last row (hidden 1024, bf16 "
+                 "in, f32 out), 12 batches of 64 texts")
+        return label, "pool_last_kernel<bf16>", len(launches), timed(launches), sum(lens), nbytes, "bf16"
+    if name == "pool_mean":
+        # config 3: mean over each text's rows (hidden 768, bf16) + L2
+        lens = w.uniform_lengths(32, 64, 8192)
+        cu = torch.tensor(w.cu_seqlens(lens), dtype=torch.int32, device=dev)
+        h = torch.randn(int(sum(lens)), 768, generator=g, device=dev).to(torch.bfloat16)
+        launches = [lambda: inl_hip.pool_mean(h, cu, normalize=True, stream=stream)]
+        nbytes = int(sum(lens)) * 768 * 2 + len(lens) * 768 * 4 + (len(lens) + 1) * 4
+        label = (f"config3 mean epilogue: mean over {sum(lens)} rows of 32 texts U[64,8192] (hidden 768, bf16 "
+                 "in, f32 out) + L2")
+        return label, "pool_mean_kernel<bf16>", 1, timed(launches), sum(lens), nbytes, "bf16"
+    if name == "splade":
+        # config 4: SPLADE max-pool over every speaking row's f32 logits
+        # (vocab 50002) of 128 texts U[32,2048], finish, fold to 36282 terms
+        lens = w.uniform_lengths(128, 32, 2048)
+        speak = [t - 1 for t in lens]
+        offs = torch.tensor(w.cu_seqlens(speak), dtype=torch.int32, device=dev)
+        S, V, terms = int(sum(speak)), 50002, 36282
+        logits = torch.empty(S, V, device=dev)
+        logits.normal_(0.0, 4.0, generator=g)
+        bias = torch.randn(V, generator=g, device=dev)
+        import numpy as np
+        rng = np.random.default_rng(0)
+        canonical = torch.from_numpy(np.concatenate([rng.permutation(terms), rng.integers(0, terms, V - terms)])
+                                     .astype(np.int32)).to(dev)
+        launches = [lambda: inl_hip.pool_splade(logits, offs, bias=bias, shift=10.0, masked_ids=(50000, 50001),
+                                                canonical=canonical, out_dim=terms, stream=stream)]
+        nbytes = S * V * 4 + V * 4 + V * 4 + len(lens) * terms * 4
+        label = (f"config4 SPLADE epilogue: max over {S} speaking rows x {V} f32 logits of 128 texts "
+                 f"U[32,2048], finish (shift 10), fold to {terms} terms")
+        return label, "splade_kernel", 1, timed(launches), S, nbytes, "f32"
+    raise SystemExit(f"unknown op workload {name}")
+
+
+def op_main(args):
+    import torch
+    import inl_hip
+    dev = torch.device("cuda:0")
+    label, kernel, n_launch, step, tokens, nbytes, dtype = op_workload(args.workload, torch, inl_hip, dev)
+    log(f"workload: {label}; {nbytes / 1e9:.3f} GB per step, {n_launch} launches")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+               for _ in range(n_launch)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(events[s])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = sum(a.elapsed_time(b) for ev in events for a, b in ev)
+    avg_ms = kernel_ms / (args.steps * n_launch)
+    gbs = nbytes / n_launch / (avg_ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": f"{args.workload} op throughput (HBM GB/s vs 8 TB/s)",
+        "value": round(tokens * args.steps / wall, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic (seeded random inputs; no checkpoint)",
+        "config": {"workload": label, "tokens_per_step": tokens, "launches_per_step": n_launch,
+                   "hbm_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernel,
+                     "avg_launch_us": round(avg_ms * 1e3, 2),
+                     "algorithmic_per_launch": {"hbm_bytes": nbytes / n_launch}},
+    }), flush=True)
 
 
 def main():
@@ -186,6 +342,10 @@ def main():
               "the path shards by independent texts, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload in OP_WORKLOADS:
+        op_main(args)
+        return
+
     import torch
     import inl_hip
     from inl_hip import attention_flops
@@ -204,12 +364,7 @@ def main():
     flops = sum(attention_flops(b, hq, d, causal, window) for b in batches)
     # algorithmic HBM bytes: Q, K, V read once and O written once, bf16
     hbm_bytes = tokens * (2 * hq * d + 2 * 2 * hkv * d + 2 * hq * d)
-    bn = plans[0].info()["block_n"]
-    kernel = (f"attn_pp_kernel<{d}, {bn}>" if d == 128
-              else f"attn_wide_kernel<{d}, {bn}>" if d == 256
-              else f"attn_pp64_kernel<{bn}>" if d == 64 and hq == hkv and hq % 2 == 0
-              else f"attn_bf16_kernel<{d}, {bn}, 4>" if d == 64
-              else f"attn_fwd_kernel<bf16, {d}, {bn}>")
+    kernel = inl_hip.kernel_name(plans[0].desc)
     n_launch = len(batches)
     stream = torch.cuda.current_stream()
     log(f"workload: {label}; {flops / 1e12:.4f} TFLOP per step, {n_launch} launches")
@@ -239,9 +394,6 @@ def main():
     avg_launch_ms = kernel_ms / (args.steps * n_launch)
     achieved = flops / n_launch / (avg_launch_ms * 1e-3) / 1e12
     achieved_gbs = hbm_bytes / n_launch / (avg_launch_ms * 1e-3) / 1e9
-    # the binding roofline is the one with the larger lower bound on time
-    mfma_floor = flops / (PEAK_BF16_TFLOPS * 1e12)
-    hbm_floor = hbm_bytes / (PEAK_HBM_GBS * 1e9)
     tok_s = tokens * args.steps / wall
     traffic = read_traffic(args.workload)
     log(f"wall {wall:.4f} s for {args.steps} steps; kernel {kernel_ms:.3f} ms; "
@@ -261,11 +413,14 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v after RMSNorm; no checkpoint)",
         "config": {"workload": label, "tokens_per_step": tokens, "launches_per_step": n_launch,
-                   "attention_tflop_per_step": round(flops / 1e12, 6)},
+                   "attention_tflop_per_step": round(flops / 1e12, 6),
+                   "value_is": ("attention-op tokens/s: tokens passed through ONE attention layer per "
+                                "second (a step runs the op once over every batch), not end-to-end "
+                                "encoded tokens/s")},
         "attention_tflops": round(flops * args.steps / wall / 1e12, 2),
         "attention_frac_of_peak": round(flops * args.steps / wall / 1e12 / PEAK_BF16_TFLOPS, 4),
-        "roofline": roofline(hbm_floor >= mfma_floor, achieved, achieved_gbs, traffic, kernel,
-                             avg_launch_ms, flops / n_launch, hbm_bytes / n_launch),
+        "roofline": roofline(achieved, achieved_gbs, traffic, kernel, avg_launch_ms, flops / n_launch,
+                             hbm_bytes / n_launch),
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale,

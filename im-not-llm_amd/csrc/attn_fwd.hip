@@ -44,6 +44,7 @@
 #include <mutex>
 #include <new>
 #include <queue>
+#include <set>
 #include <unordered_map>
 #include <vector>
 
@@ -105,7 +106,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
   const int seg = it.x;
   const int T = it.y;
   const int q0 = it.z;
-  const int lo_t = it.w >> 16;
+  const int lo_t = (int)((uint32_t)it.w >> 16);
   const int hi_t = it.w & 0xffff;
   const int kvh = hg / p.groups_per_kv;
   const int head = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + wave / p.rb;
@@ -426,11 +427,13 @@ struct KernelCfg {
   int rows;     // query rows per wave (32 or 64)
   bool persistent = false;  // one workgroup per CU over a host-assigned unit list
   bool head_pairs = false;  // a unit serves two query heads with their own K/V (group 1)
+  const char* name = "";    // kernel name, for reporting
 };
 
 template <typename E, int D, int BN, int NW, bool PV16>
-KernelCfg make_cfg() {
-  return KernelCfg{attn_fwd_kernel<E, D, BN, NW, PV16>, D, BN, NW, 4 * BN * D * (int)sizeof(E), 32};
+KernelCfg make_cfg(const char* name) {
+  return KernelCfg{attn_fwd_kernel<E, D, BN, NW, PV16>, D, BN, NW, 4 * BN * D * (int)sizeof(E), 32, false, false,
+                   name};
 }
 
 // `fits32`: every text's q/k/v rows span < 4 GiB, as the fast kernel's
@@ -442,27 +445,37 @@ int select_kernel(int32_t dtype, int32_t head_dim, int32_t flags, bool fits32, i
     AttnKernelFn fn;
     int bn, nw, lds;
     if (group == 1 && h_q % 2 == 0 && bf16_pp64_kernel(head_dim, &fn, &bn, &nw, &lds)) {
-      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true, true};
+      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true, true, "attn_pp64_kernel<64, 64>"};
       return INL_OK;
     }
-    if (bf16_pp_kernel(head_dim, &fn, &bn, &nw, &lds) || bf16_wide_kernel(head_dim, &fn, &bn, &nw, &lds)) {
-      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true};
+    if (bf16_pp_kernel(head_dim, &fn, &bn, &nw, &lds)) {
+      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true, false, "attn_pp_kernel<128, 64>"};
+      return INL_OK;
+    }
+    if (bf16_wide_kernel(head_dim, &fn, &bn, &nw, &lds)) {
+      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, true, false, "attn_wide_kernel<256, 32>"};
       return INL_OK;
     }
     if (bf16_fast_kernel(head_dim, &fn, &bn, &nw, &lds)) {
-      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32};
+      *cfg = KernelCfg{fn, head_dim, bn, nw, lds, 32, false, false, "attn_bf16_kernel<64, 64, 4>"};
       return INL_OK;
     }
   }
   if (dtype == INL_BF16) {
-    if (head_dim <= 64) *cfg = pv16 ? make_cfg<bf16, 64, 64, 4, true>() : make_cfg<bf16, 64, 64, 4, false>();
-    else if (head_dim <= 128) *cfg = pv16 ? make_cfg<bf16, 128, 64, 4, true>() : make_cfg<bf16, 128, 64, 4, false>();
-    else if (head_dim <= 256) *cfg = pv16 ? make_cfg<bf16, 256, 64, 4, true>() : make_cfg<bf16, 256, 64, 4, false>();
+    if (head_dim <= 64)
+      *cfg = pv16 ? make_cfg<bf16, 64, 64, 4, true>("attn_fwd_kernel<bf16, 64, 64, 4, pv16>")
+                  : make_cfg<bf16, 64, 64, 4, false>("attn_fwd_kernel<bf16, 64, 64, 4, pv_bf16>");
+    else if (head_dim <= 128)
+      *cfg = pv16 ? make_cfg<bf16, 128, 64, 4, true>("attn_fwd_kernel<bf16, 128, 64, 4, pv16>")
+                  : make_cfg<bf16, 128, 64, 4, false>("attn_fwd_kernel<bf16, 128, 64, 4, pv_bf16>");
+    else if (head_dim <= 256)
+      *cfg = pv16 ? make_cfg<bf16, 256, 64, 4, true>("attn_fwd_kernel<bf16, 256, 64, 4, pv16>")
+                  : make_cfg<bf16, 256, 64, 4, false>("attn_fwd_kernel<bf16, 256, 64, 4, pv_bf16>");
     else return fail(INL_E_UNSUPPORTED, "attention: head_dim > 256 is not supported");
   } else {
-    if (head_dim <= 64) *cfg = make_cfg<float, 64, 64, 4, false>();
-    else if (head_dim <= 128) *cfg = make_cfg<float, 128, 64, 4, false>();
-    else if (head_dim <= 256) *cfg = make_cfg<float, 256, 32, 4, false>();
+    if (head_dim <= 64) *cfg = make_cfg<float, 64, 64, 4, false>("attn_fwd_kernel<f32, 64, 64, 4>");
+    else if (head_dim <= 128) *cfg = make_cfg<float, 128, 64, 4, false>("attn_fwd_kernel<f32, 128, 64, 4>");
+    else if (head_dim <= 256) *cfg = make_cfg<float, 256, 32, 4, false>("attn_fwd_kernel<f32, 256, 32, 4>");
     else return fail(INL_E_UNSUPPORTED, "attention: head_dim > 256 is not supported");
   }
   return INL_OK;
@@ -712,7 +725,11 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
   const int64_t qs = d->q_row_stride ? d->q_row_stride : (int64_t)d->h_q * d->head_dim;
   const int64_t ks = d->k_row_stride ? d->k_row_stride : (int64_t)d->h_kv * d->head_dim;
   const int64_t vs = d->v_row_stride ? d->v_row_stride : (int64_t)d->h_kv * d->head_dim;
-  const int64_t widest = std::max(qs, std::max(ks, vs)) * es;
+  const int64_t os = d->o_row_stride ? d->o_row_stride : (int64_t)d->h_q * d->head_dim;
+  // The persistent kernels address each text's q, k, v and out rows with
+  // 32-bit buffer offsets; the output row (f32 out is twice a bf16 input
+  // row, and a caller stride may be wider) counts like the input rows.
+  const int64_t widest = std::max(std::max(qs, std::max(ks, vs)) * es, os * dtype_size(d->out_dtype));
   const bool fits32 = (max_t + 256) * widest < ((int64_t)1 << 32);
   int rc = select_kernel(d->dtype, d->head_dim, d->flags, fits32, d->h_q, d->h_q / d->h_kv, &s->cfg);
   if (rc) return rc;
@@ -740,6 +757,8 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
         hi = std::min(hi, qlast + d->window + 1);
       }
       const int lo_t = lo / BN, hi_t = (hi + BN - 1) / BN;
+      if (hi_t > 0xffff)
+        return fail(INL_E_UNSUPPORTED, "attention: a text spans more than 65535 key tiles");
       tmp.push_back({make_int4(seg, T, q0, (lo_t << 16) | hi_t), hi_t - lo_t});
     }
   }
@@ -784,17 +803,27 @@ AttnParams make_params(const inl_attn_desc* d, const Schedule& s, const void* de
   return p;
 }
 
+// The dynamic LDS limit of a kernel is raised once per (kernel, device):
+// plans do it when they are created, the one-shot forms before their first
+// launch on a device. Launches then take no lock.
 std::mutex g_attr_mu;
+std::set<std::pair<const void*, int>> g_attr_done;
+
+int ensure_lds_attr(const KernelCfg& cfg) {
+  int dev = 0;
+  INL_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_attr_mu);
+  if (g_attr_done.count({(const void*)cfg.fn, dev})) return INL_OK;
+  INL_HIP_TRY(hipFuncSetAttribute((const void*)cfg.fn, hipFuncAttributeMaxDynamicSharedMemorySize, cfg.lds));
+  g_attr_done.insert({(const void*)cfg.fn, dev});
+  return INL_OK;
+}
 
 int launch(const Schedule& s, const AttnParams& p, hipStream_t stream) {
   const KernelCfg& cfg = s.cfg;
   const int64_t blocks = s.grid();
   if (blocks <= 0) return INL_OK;
   if (blocks > 0x7fffffff) return fail(INL_E_UNSUPPORTED, "attention: too many tiles for one launch");
-  {
-    std::lock_guard<std::mutex> lock(g_attr_mu);
-    INL_HIP_TRY(hipFuncSetAttribute((const void*)cfg.fn, hipFuncAttributeMaxDynamicSharedMemorySize, cfg.lds));
-  }
   hipLaunchKernelGGL(cfg.fn, dim3((unsigned)blocks), dim3(cfg.nw * 64), cfg.lds, stream, p);
   INL_HIP_TRY(hipGetLastError());
   return INL_OK;
@@ -812,6 +841,26 @@ int check_ptrs(const void* q, const void* k, const void* v, const void* out, int
 
 }  // namespace
 
+}  // namespace inl
+
+namespace inl {
+namespace {
+
+// Upload a schedule into device memory `buf` (a caller workspace) and
+// launch. The schedule is copied from ordinary (pageable) host memory:
+// hipMemcpyAsync takes the data before it returns, so nothing pinned is
+// allocated; the copy orders behind the stream's earlier work.
+int launch_one_shot(const inl_attn_desc* desc, const Schedule& s, void* buf, const void* q, const void* k,
+                    const void* v, void* out, hipStream_t stream) {
+  int rc = ensure_lds_attr(s.cfg);
+  if (rc) return rc;
+  const std::vector<char> blob = s.pack();
+  INL_HIP_TRY(hipMemcpyAsync(buf, blob.data(), blob.size(), hipMemcpyHostToDevice, stream));
+  AttnParams p = make_params(desc, s, buf, q, k, v, out);
+  return launch(s, p, stream);
+}
+
+}  // namespace
 }  // namespace inl
 
 struct inl_attn_plan {
@@ -835,6 +884,8 @@ extern "C" int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** p
   pl->desc.seq_starts_host = nullptr;
   pl->total_tokens = total;
   rc = build_schedule(desc, &pl->sched);
+  if (rc) { delete pl; return rc; }
+  rc = ensure_lds_attr(pl->sched.cfg);
   if (rc) { delete pl; return rc; }
   const std::vector<char> blob = pl->sched.pack();
   if (!blob.empty()) {
@@ -907,9 +958,19 @@ extern "C" int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q, con
   if (!workspace || workspace_bytes < need)
     return fail(INL_E_INVALID, "attention: workspace is NULL or smaller than inl_attn_workspace_size()");
   if (!aligned16(workspace)) return fail(INL_E_INVALID, "attention: workspace must be 16-byte aligned");
-  const std::vector<char> blob = s.pack();
-  rc = upload_async(workspace, blob.data(), need, (hipStream_t)stream);
+  return launch_one_shot(desc, s, workspace, q, k, v, out, (hipStream_t)stream);
+}
+
+extern "C" int inl_attn_kernel_name(const inl_attn_desc* desc, const char** name) {
+  using namespace inl;
+  if (!name) return fail(INL_E_INVALID, "attention: name out-pointer is NULL");
+  *name = nullptr;
+  int64_t total = 0;
+  int rc = validate_desc(desc, &total);
   if (rc) return rc;
-  AttnParams p = make_params(desc, s, workspace, q, k, v, out);
-  return launch(s, p, (hipStream_t)stream);
+  Schedule s;
+  rc = build_schedule(desc, &s);
+  if (rc) return rc;
+  *name = s.cfg.name;
+  return INL_OK;
 }

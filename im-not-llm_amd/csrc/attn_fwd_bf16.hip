@@ -75,7 +75,7 @@ __global__ __launch_bounds__(NW * 64, D >= 256 ? 1 : 2) void attn_bf16_kernel(At
   const int seg = it.x;
   const int T = it.y;
   const int q0 = it.z;
-  const int lo_t = it.w >> 16;
+  const int lo_t = (int)((uint32_t)it.w >> 16);
   const int hi_t = it.w & 0xffff;
   const int kvh = hg / p.groups_per_kv;
   const int head = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + wave / p.rb;

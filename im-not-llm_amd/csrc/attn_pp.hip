@@ -107,7 +107,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     seg = __builtin_amdgcn_readfirstlane(d.x);
     T = __builtin_amdgcn_readfirstlane(d.y);
     q0 = __builtin_amdgcn_readfirstlane(d.z);
-    lo = __builtin_amdgcn_readfirstlane(d.w) >> 16;
+    lo = (int)((uint32_t)__builtin_amdgcn_readfirstlane(d.w) >> 16);
     hi = __builtin_amdgcn_readfirstlane(d.w) & 0xffff;
     hg = __builtin_amdgcn_readfirstlane(shg[u]);
   };

@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
     seg = __builtin_amdgcn_readfirstlane(d.x);
     T = __builtin_amdgcn_readfirstlane(d.y);
     q0 = __builtin_amdgcn_readfirstlane(d.z);
-    lo = __builtin_amdgcn_readfirstlane(d.w) >> 16;
+    lo = (int)((uint32_t)__builtin_amdgcn_readfirstlane(d.w) >> 16);
     hi = __builtin_amdgcn_readfirstlane(d.w) & 0xffff;
     hg = __builtin_amdgcn_readfirstlane(shg[u]);
   };
@@ -192,8 +192,14 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
     for (int i = 0; i < KST; ++i)
       qreg[i] = __builtin_amdgcn_raw_buffer_load_b128(qrs, qrow_b + (2 * i + hf) * 16, 0, 0);
   };
-  // Q^T of unit u from inline asm (untracked by the compiler, like the K/V
-  // loads); the end-of-iteration wait takes qreg as operands.
+  // Q^T of unit u, loaded into qreg once the current unit's last QK^T has
+  // read it. The 16 loads and a full wait form ONE asm statement, so every
+  // value is complete before the compiler can use or copy it: with ~450
+  // registers live it moves Q^T between VGPRs and AGPRs, and a copy of a
+  // register whose load is still in flight would take stale data (which is
+  // what a load-now, wait-later form produced). The outputs are AGPRs, where
+  // the allocator keeps Q^T as the QK^T MFMAs' B operand. The wait also
+  // retires the K/V loads issued before it; it stalls once per unit.
   auto load_q_of = [&](int u) __attribute__((always_inline)) {
     int sg, tn, q0, lo, hi, hg;
     unit(u, sg, tn, q0, lo, hi, hg);
@@ -201,19 +207,34 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
     const int hd = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + wave / p.rb;
     const i32x4 rs = pp_rsrc_words(p.q + ((int64_t)sg * p.q_stride + (int64_t)hd * D) * 2, (uint32_t)tn * qst_b);
     const uint32_t qa = (uint32_t)(q0 + (wave % p.rb) * 32 + lq) * qst_b + hf * 16;
-#pragma unroll
-    for (int i = 0; i < KST; ++i)
-      asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
-                   : "=v"(qreg[i]) : "v"(qa), "s"(rs), "n"(32 * i) : "memory");
+    static_assert(KST == 16, "the asm below loads sixteen Q registers");
+    asm volatile(
+        "buffer_load_dwordx4 %0, %16, %17, 0 offen offset:0\n\t"
+        "buffer_load_dwordx4 %1, %16, %17, 0 offen offset:32\n\t"
+        "buffer_load_dwordx4 %2, %16, %17, 0 offen offset:64\n\t"
+        "buffer_load_dwordx4 %3, %16, %17, 0 offen offset:96\n\t"
+        "buffer_load_dwordx4 %4, %16, %17, 0 offen offset:128\n\t"
+        "buffer_load_dwordx4 %5, %16, %17, 0 offen offset:160\n\t"
+        "buffer_load_dwordx4 %6, %16, %17, 0 offen offset:192\n\t"
+        "buffer_load_dwordx4 %7, %16, %17, 0 offen offset:224\n\t"
+        "buffer_load_dwordx4 %8, %16, %17, 0 offen offset:256\n\t"
+        "buffer_load_dwordx4 %9, %16, %17, 0 offen offset:288\n\t"
+        "buffer_load_dwordx4 %10, %16, %17, 0 offen offset:320\n\t"
+        "buffer_load_dwordx4 %11, %16, %17, 0 offen offset:352\n\t"
+        "buffer_load_dwordx4 %12, %16, %17, 0 offen offset:384\n\t"
+        "buffer_load_dwordx4 %13, %16, %17, 0 offen offset:416\n\t"
+        "buffer_load_dwordx4 %14, %16, %17, 0 offen offset:448\n\t"
+        "buffer_load_dwordx4 %15, %16, %17, 0 offen offset:480\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&a"(qreg[0]), "=&a"(qreg[1]), "=&a"(qreg[2]), "=&a"(qreg[3]), "=&a"(qreg[4]), "=&a"(qreg[5]),
+          "=&a"(qreg[6]), "=&a"(qreg[7]), "=&a"(qreg[8]), "=&a"(qreg[9]), "=&a"(qreg[10]), "=&a"(qreg[11]),
+          "=&a"(qreg[12]), "=&a"(qreg[13]), "=&a"(qreg[14]), "=&a"(qreg[15])
+        : "v"(qa), "s"(rs)
+        : "memory");
   };
   auto wait_loads = [&]() __attribute__((always_inline)) {
-    // all but this iteration's K/V loads; Q loads issued before them are in
-    static_assert(KST == 16, "the wait below names sixteen Q registers");
-    asm volatile("s_waitcnt vmcnt(%16)"
-                 : "+v"(qreg[0]), "+v"(qreg[1]), "+v"(qreg[2]), "+v"(qreg[3]), "+v"(qreg[4]), "+v"(qreg[5]),
-                   "+v"(qreg[6]), "+v"(qreg[7]), "+v"(qreg[8]), "+v"(qreg[9]), "+v"(qreg[10]), "+v"(qreg[11]),
-                   "+v"(qreg[12]), "+v"(qreg[13]), "+v"(qreg[14]), "+v"(qreg[15])
-                 : "n"(DMA_PARTS) : "memory");
+    // all but this iteration's K/V loads
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(DMA_PARTS) : "memory");
   };
 
   f32x16 oacc[NDB];
@@ -472,8 +493,6 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
     __builtin_amdgcn_sched_barrier(0);
 
     // the next unit's Q, once the last QK^T of the current one is issued
-    // (before this iteration's K/V loads, so the end-of-iteration wait
-    // covers it)
     if (__builtin_expect(qt + 1 == qhi && qu + 1 < nu, 0)) load_q_of(qu + 1);
 
     // PV of tile j beside the conversion of tile j + 1 and the loads of tile j + 3

@@ -41,8 +41,4 @@ inline bool dtype_ok(int32_t dt) { return dt == INL_F32 || dt == INL_BF16; }
 // count through `total`.
 int check_cu(int32_t n, const int32_t* cu, int64_t* total);
 
-// Copy a small host buffer to device memory on `stream` through the calling
-// thread's pinned staging buffer; `src` may be released when this returns.
-int upload_async(void* dst, const void* src, size_t bytes, hipStream_t stream);
-
 }  // namespace inl

@@ -151,9 +151,11 @@ __global__ __launch_bounds__(256) void splade_kernel(SpladeParams p) {
   x = open ? x : 0.f;
   const float w = logf(x + 1.0f);
   if (p.canonical) {
-    // w >= 0: unsigned order of the bits is the float order
-    atomicMax(reinterpret_cast<unsigned int*>(p.out + (int64_t)r * p.out_dim + p.canonical[t]),
-              __float_as_uint(w));
+    // w >= 0: unsigned order of the bits is the float order. An id outside
+    // [0, out_dim) is skipped rather than written out of bounds.
+    const uint32_t c = (uint32_t)p.canonical[t];
+    if (c < (uint32_t)p.out_dim)
+      atomicMax(reinterpret_cast<unsigned int*>(p.out + (int64_t)r * p.out_dim + c), __float_as_uint(w));
   } else {
     p.out[(int64_t)r * p.out_dim + t] = w;
   }

@@ -108,6 +108,8 @@ _ws_size = _sig("inl_attn_workspace_size", ctypes.c_int, ctypes.POINTER(AttnDesc
 _varlen_fwd = _sig("inl_attn_varlen_fwd", ctypes.c_int, ctypes.POINTER(AttnDesc),
                    c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_size_t,
                    c_void_p)
+_kernel_name = _sig("inl_attn_kernel_name", ctypes.c_int, ctypes.POINTER(AttnDesc),
+                    ctypes.POINTER(ctypes.c_char_p))
 
 
 _norm_rope = _sig("inl_norm_rope_fwd", ctypes.c_int, ctypes.POINTER(NormRopeDesc), c_void_p,
@@ -156,6 +158,7 @@ def exported_symbols() -> list:
     names = []
     for n in ("inl_attn_plan_create", "inl_attn_plan_destroy", "inl_attn_plan_info",
               "inl_attn_fwd", "inl_attn_workspace_size", "inl_attn_varlen_fwd",
+              "inl_attn_kernel_name",
               "inl_norm_rope_fwd", "inl_rope_table_host", "inl_positions_host", "inl_pool_last_fwd",
               "inl_pool_mean_fwd", "inl_l2_normalize_fwd", "inl_pool_splade_fwd",
               "inl_last_error", "inl_abi_version"):
@@ -215,6 +218,53 @@ def make_attn_desc(cu_seqlens, h_q, h_kv, head_dim, *, causal, window=-1, scale=
     return d
 
 
+def desc_rows(desc: AttnDesc) -> int:
+    """Rows of q, k, v and out that ``desc`` reads or writes: the packed
+    total ``cu_seqlens[-1]``, or with ``seq_starts`` the end of the last text."""
+    n = desc.n_texts
+    if n <= 0:
+        return 0
+    cu = desc.cu_seqlens_host
+    if desc.seq_starts_host:
+        st = desc.seq_starts_host
+        return max(int(st[b]) + int(cu[b + 1]) - int(cu[b]) for b in range(n))
+    return int(cu[n])
+
+
+def kernel_name(desc: AttnDesc) -> str:
+    """The kernel a plan for ``desc`` launches (``inl_attn_kernel_name``)."""
+    name = ctypes.c_char_p()
+    _check(_kernel_name(ctypes.byref(desc), ctypes.byref(name)))
+    return name.value.decode()
+
+
+def _check_tensors(desc: AttnDesc, q, k, v, out) -> None:
+    """Refuse tensors the kernels would read or write past: every tensor must
+    hold the rows ``desc`` covers, with its dtype and row strides, and live on a
+    GPU. The library sees only pointers, so these checks are the binding's."""
+    import torch
+    rows = desc_rows(desc)
+    want_in = torch.bfloat16 if desc.dtype == INL_BF16 else torch.float32
+    want_out = torch.bfloat16 if desc.out_dtype == INL_BF16 else torch.float32
+    d = desc.head_dim
+    specs = (("q", q, desc.h_q, desc.q_row_stride, want_in), ("k", k, desc.h_kv, desc.k_row_stride, want_in),
+             ("v", v, desc.h_kv, desc.v_row_stride, want_in), ("out", out, desc.h_q, desc.o_row_stride, want_out))
+    for name, t, heads, stride, dt in specs:
+        if t.dtype != dt:
+            raise InlError(-1, f"{name}: dtype {t.dtype}, the desc needs {dt}")
+        if t.dim() != 3 or t.shape[1] != heads or t.shape[2] != d:
+            raise InlError(-1, f"{name}: shape {tuple(t.shape)}, the desc needs [rows, {heads}, {d}]")
+        if t.stride(2) != 1 or t.stride(1) != d:
+            raise InlError(-1, f"{name}: heads must be contiguous inside a token row")
+        if t.shape[0] < rows:
+            raise InlError(-1, f"{name}: {t.shape[0]} rows, the desc covers {rows}")
+        if rows > 0 and t.stride(0) != (stride if stride else heads * d):
+            raise InlError(-1, f"{name}: row stride {t.stride(0)} differs from the desc's")
+    for name, t, _, _, _ in specs:
+        if not t.is_cuda:
+            raise InlError(-1, f"{name}: not a device tensor")
+
+
 class AttnPlan:
     """A device-resident tile schedule for one packed batch and one attention
     form (``inl_attn_plan_create``); reusable across layers of that form."""
@@ -224,6 +274,7 @@ class AttnPlan:
         h = c_void_p()
         _check(_plan_create(ctypes.byref(desc), ctypes.byref(h)))
         self._h = h
+        self.rows = desc_rows(desc)
 
     @property
     def handle(self) -> int:
@@ -238,6 +289,7 @@ class AttnPlan:
 
     def run(self, q, k, v, out, stream=None) -> None:
         """Enqueue ``out = attention(q, k, v)`` (torch device tensors)."""
+        _check_tensors(self.desc, q, k, v, out)
         _check(_attn_fwd(self._h, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                          out.data_ptr(), _stream_ptr(stream)))
 
@@ -274,9 +326,7 @@ def varlen_attention(q, k, v, cu_seqlens, *, causal: bool, window: int = -1,
                           q_row_stride=q.stride(0), k_row_stride=k.stride(0),
                           v_row_stride=v.stride(0), o_row_stride=out.stride(0), flags=flags,
                           seq_starts=seq_starts)
-    for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
-        if t.stride(2) != 1 or t.stride(1) != d:
-            raise InlError(-1, f"{name}: heads must be contiguous inside a token row")
+    _check_tensors(desc, q, k, v, out)
     nbytes = ctypes.c_size_t()
     _check(_ws_size(ctypes.byref(desc), ctypes.byref(nbytes)))
     ws = torch.empty(max(16, nbytes.value), dtype=torch.uint8, device=q.device)

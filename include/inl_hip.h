@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define INL_HIP_ABI_VERSION 1
+#define INL_HIP_ABI_VERSION 2
 
 enum inl_status {
   INL_OK = 0,
@@ -92,9 +92,15 @@ typedef struct inl_attn_desc {
   const int32_t* seq_starts_host;
 } inl_attn_desc;
 
-/* bf16 inputs: the PV product runs in fp16 by default (V converted exactly
- * while staged, P rounded to fp16: |v| must stay below 65504, larger values
- * become inf). This flag keeps V and P in bf16 (any range, 8x coarser P). */
+/* bf16 inputs: the PV product runs in fp16 by default. V is converted to
+ * fp16 while staged: exact for 2^-14 <= |v| < 65520 (bf16's 8 significant
+ * bits fit fp16's 11); smaller values round to fp16 subnormals (absolute
+ * error <= 2^-25); |v| >= 65520 becomes inf: the rows that see such a key
+ * come out inf or NaN, and so may other rows of the same text (a masked
+ * weight 0 times inf is NaN); other texts are unaffected. P is rounded to
+ * fp16. Callers whose V is not normalised (Qwen3, ModernBERT, Qwen3.5: V
+ * straight from the projection) and can reach 65520 set this flag, which
+ * keeps V and P in bf16 (any range, 8x coarser P). */
 #define INL_ATTN_PV_BF16 1
 
 /* An attention plan: the packed texts' tile schedule, resident on the
@@ -103,7 +109,9 @@ typedef struct inl_attn_desc {
 typedef struct inl_attn_plan inl_attn_plan;
 
 /* Build a plan (host work + one blocking upload). The desc's pointer fields
- * are read during the call only. */
+ * are read during the call only. The plan belongs to the device that is
+ * current when it is created: its schedule lives there, and the kernel's
+ * launch attributes are set there once, so inl_attn_fwd takes no lock. */
 int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** plan);
 int inl_attn_plan_destroy(inl_attn_plan* plan);
 /* Tiles the plan launches and query rows each covers (for reporting). */
@@ -115,11 +123,21 @@ int inl_attn_fwd(const inl_attn_plan* plan, const void* q, const void* k,
                  const void* v, void* out, void* stream);
 
 /* One-shot form: plans into `workspace` (device memory of at least
- * inl_attn_workspace_size() bytes) and launches. */
+ * inl_attn_workspace_size() bytes, 16-byte aligned) and launches. It
+ * allocates no device or pinned memory: the schedule is built in host memory
+ * and copied into the workspace with hipMemcpyAsync from pageable memory,
+ * which orders behind the stream's earlier work. The workspace must stay
+ * untouched until the launch has completed on `stream`. */
 int inl_attn_workspace_size(const inl_attn_desc* desc, size_t* bytes);
 int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q,
                         const void* k, const void* v, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Host only: the name of the kernel a plan for `desc` launches (a static
+ * string, e.g. "attn_pp_kernel<128, 64>"), for reporting and tests. The
+ * bf16 fast kernels address each text's rows with 32-bit offsets; a text
+ * whose q, k, v or out rows span 4 GiB or more takes the generic kernel. */
+int inl_attn_kernel_name(const inl_attn_desc* desc, const char** name);
 
 /* ------------------------------------------------------------------------
  * Prologue: fused per-head RMSNorm + RoPE over packed rows.
@@ -224,6 +242,8 @@ int inl_l2_normalize_fwd(int32_t rows, int32_t dim, int64_t in_stride,
  *   out[r, c] = max(0, max over t with canonical[t] == c of w[r, t])
  *               (canonical NULL: out = w and out_dim == vocab).
  * offs: DEVICE int32 [rows + 1]. bias NULL = no bias. out: [rows, out_dim].
+ * canonical: DEVICE int32 [vocab] with 0 <= canonical[t] < out_dim; an id
+ * outside that range is skipped (its term is dropped, nothing is written). 
  * The max and the fold do not depend on evaluation order: for given logits
  * the output, and its active-term set {c : out > 0}, is bit-exact. */
 int inl_pool_splade_fwd(int32_t rows, const int32_t* offs, int32_t vocab,

@@ -11,12 +11,19 @@ implementation performs on the encoder attention hot path:
 * ``prologue``   - per-head RMSNorm and the half-split / partial / axial RoPE;
 * ``pooling``    - last-token, mean and SPLADE epilogues, L2 normalisation,
   Matryoshka truncation and the sparse active-term set;
-* ``tiny_models`` - the tiny EmbeddingGemma 2 and ModernBERT-SPLADE encoders
-  of the reference's golden fixtures, used to pin the forms above in situ;
 * ``planner``    - the reference's padded batch planner, its packed
   counterpart and a brute-force optimum for small inputs;
 * ``cref``       - a ctypes loader for ``attn_ref.c``, the multi-threaded f32
   C restatement used as the CPU baseline.
+
+The tiny EmbeddingGemma 2 and ModernBERT-SPLADE encoders that run the
+reference's golden fixtures over these functions (pinning the forms in situ)
+live beside the tests, in ``tests/tiny_encoders.py``.
+
+Parity unpinned: none of the functions here. Each is checked against the
+reference's known answers, its golden fixtures or a closed form in
+``tests/test_oracle_*.py``; the RoPE tables and the partial and axial
+rotations in ``tests/test_oracle_rope_pins.py``.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg may import this package, and only as the checker: the

@@ -35,8 +35,14 @@ static void attend_row(const float* qi, const float* kbase, const float* vbase,
     float bm = -INFINITY;
     for (int j = j0; j < j1; ++j) {
       const float* kj = kbase + (int64_t)j * kv_stride;
-      float dot = 0.f;
-      for (int e = 0; e < d; ++e) dot += qi[e] * kj[e];
+      /* eight interleaved partial sums in a fixed order, so the compiler
+       * can use 8-wide vector FMAs without reassociating (no fast-math) */
+      float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      int e = 0;
+      for (; e + 8 <= d; e += 8)
+        for (int u = 0; u < 8; ++u) part[u] += qi[e + u] * kj[e + u];
+      for (; e < d; ++e) part[e & 7] += qi[e] * kj[e];
+      float dot = ((part[0] + part[4]) + (part[2] + part[6])) + ((part[1] + part[5]) + (part[3] + part[7]));
       dot *= scale;
       s[j - j0] = dot;
       if (dot > bm) bm = dot;

@@ -22,7 +22,7 @@ def test_every_declared_symbol_is_exported():
     assert len(declared) >= 15
     missing = [n for n in declared if not hasattr(lib, n)]
     assert not missing, f"declared but not exported: {missing}"
-    assert inl_hip.abi_version() == 1
+    assert inl_hip.abi_version() == 2
 
 
 def test_attention_desc_validation_errors():
@@ -71,3 +71,73 @@ def test_host_helpers_validate():
         inl_hip.rope_table(7, 1e4, 4)
     with pytest.raises(inl_hip.InlError):
         inl_hip.positions([0, 4, 2])
+
+
+def test_kernel_selection_counts_output_row_bytes():
+    """The fast kernels address a text's rows with 32-bit offsets. A Qwen3
+    text of 524,288 tokens has 4 KiB bf16 q rows (2.1 GiB per text) but 8 KiB
+    f32 output rows (4.3 GiB): it must take the generic kernel, which uses
+    64-bit offsets. The same text with bf16 output fits, and so does a short
+    text with f32 output; a wide caller output stride counts too."""
+    import inl_hip
+    long = [0, 524_288]
+    mk = lambda cu, **kw: inl_hip.make_attn_desc(cu, 16, 8, 128, causal=True, dtype="bf16", **kw)
+    assert inl_hip.kernel_name(mk(long, out_dtype="bf16")) == "attn_pp_kernel<128, 64>"
+    assert inl_hip.kernel_name(mk(long, out_dtype="f32")).startswith("attn_fwd_kernel<bf16, 128")
+    assert inl_hip.kernel_name(mk([0, 4096], out_dtype="f32")) == "attn_pp_kernel<128, 64>"
+    assert inl_hip.kernel_name(mk(long, out_dtype="bf16", o_row_stride=8192)).startswith("attn_fwd_kernel")
+    # the other fast kernels by shape
+    assert inl_hip.kernel_name(inl_hip.make_attn_desc([0, 100], 3, 1, 256, causal=False)) == \
+        "attn_wide_kernel<256, 32>"
+    assert inl_hip.kernel_name(inl_hip.make_attn_desc([0, 100], 12, 12, 64, causal=False)) == \
+        "attn_pp64_kernel<64, 64>"
+    assert inl_hip.kernel_name(inl_hip.make_attn_desc([0, 100], 12, 12, 64, causal=False, dtype="f32")) == \
+        "attn_fwd_kernel<f32, 64, 64, 4>"
+    assert inl_hip.kernel_name(inl_hip.make_attn_desc([0, 100], 16, 8, 128, causal=True,
+                                                      flags=inl_hip.ATTN_PV_BF16)).endswith("pv_bf16>")
+
+
+def test_tile_ranges_fit_their_16_bit_fields():
+    """A work item packs its first and last key tile into 16 bits each. With
+    32-key tiles (head_dim 256) a text of 2^21 - 1 tokens needs 65,536 tiles
+    and is refused; one of 2^21 - 33 tokens needs 65,535 and is planned, with
+    and without a window."""
+    import inl_hip
+    n = ctypes.c_size_t()
+    for window in (-1, 512):
+        bad = inl_hip.make_attn_desc([0, 2**21 - 1], 3, 1, 256, causal=False, window=window)
+        assert inl_hip._ws_size(ctypes.byref(bad), ctypes.byref(n)) == -2
+        assert "65535 key tiles" in inl_hip.last_error()
+        ok = inl_hip.make_attn_desc([0, 2**21 - 33], 3, 1, 256, causal=False, window=window)
+        assert inl_hip._ws_size(ctypes.byref(ok), ctypes.byref(n)) == 0, inl_hip.last_error()
+
+
+def test_binding_refuses_tensors_the_kernels_would_overrun():
+    """The library sees pointers only, so the Python binding checks that q, k,
+    v and out hold every row the desc covers, with its dtypes and strides,
+    before it calls the library (CPU tensors: the device check comes last)."""
+    import torch
+    import inl_hip
+    cu = [0, 5, 9]
+    desc = inl_hip.make_attn_desc(cu, 4, 2, 16, causal=True, dtype="bf16", out_dtype="f32")
+    mk = lambda n, h, dt=torch.bfloat16: torch.zeros(n, h, 16, dtype=dt)
+    good = (mk(9, 4), mk(9, 2), mk(9, 2), mk(9, 4, torch.float32))
+    with pytest.raises(inl_hip.InlError, match="not a device tensor"):
+        inl_hip._check_tensors(desc, *good)
+    cases = [
+        ((mk(8, 4), mk(9, 2), mk(9, 2), mk(9, 4, torch.float32)), "q: 8 rows, the desc covers 9"),
+        ((mk(9, 4), mk(9, 2), mk(7, 2), mk(9, 4, torch.float32)), "v: 7 rows"),
+        ((mk(9, 4), mk(9, 2), mk(9, 2), mk(8, 4, torch.float32)), "out: 8 rows"),
+        ((mk(9, 4), mk(9, 2, torch.float32), mk(9, 2), mk(9, 4, torch.float32)), "k: dtype"),
+        ((mk(9, 4), mk(9, 2), mk(9, 2), mk(9, 4)), "out: dtype"),
+        ((mk(9, 4), mk(9, 3), mk(9, 2), mk(9, 4, torch.float32)), "k: shape"),
+    ]
+    for tensors, msg in cases:
+        with pytest.raises(inl_hip.InlError, match=msg.replace("[", r"\[")):
+            inl_hip._check_tensors(desc, *tensors)
+    # padded batches: seq_starts move the last text's end
+    padded = inl_hip.make_attn_desc(cu, 4, 2, 16, causal=True, dtype="bf16", out_dtype="f32",
+                                    seq_starts=[0, 12])
+    assert inl_hip.desc_rows(padded) == 16
+    with pytest.raises(inl_hip.InlError, match="the desc covers 16"):
+        inl_hip._check_tensors(padded, *good)

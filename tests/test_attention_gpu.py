@@ -49,13 +49,31 @@ CASES = [
     ("qwen35_causal_d256", [1, 77, 300], 16, 2, 256, True, -1, 256 ** -0.5),
     ("causal_window", [90, 200], 4, 2, 128, True, 16, 128 ** -0.5),
     ("tiny_head_dims", [9, 13], 4, 2, 16, False, 3, 1.0),
+    # Many short texts: several work units per workgroup for every persistent
+    # kernel, so unit switches (the next unit's Q, K/V streams, output
+    # stores) are exercised with real scores (the cases above fit one unit
+    # per workgroup).
+    ("d128_many_units", "many:0:300:1:260", 16, 8, 128, True, -1, 128 ** -0.5),
+    ("d256_many_units_window", "many:1:160:1:400", 3, 1, 256, False, 96, 1.0),
+    ("d256_many_units_full", "many:2:160:1:400", 3, 1, 256, False, -1, 1.0),
+    ("d256_many_units_causal", "many:3:60:1:300", 16, 2, 256, True, -1, 256 ** -0.5),
+    ("d64_many_units", "many:4:200:1:300", 12, 12, 64, False, 64, 64 ** -0.5),
 ]
+
+
+def _lengths(spec):
+    """A literal list, or "many:seed:n:lo:hi" = n seeded lengths in [lo, hi]."""
+    if not isinstance(spec, str):
+        return spec
+    _, seed, n, lo, hi = spec.split(":")
+    return [int(x) for x in np.random.default_rng(int(seed)).integers(int(lo), int(hi) + 1, int(n))]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_bf16_matches_oracle(case, cuda, inl):
     import torch
     name, lengths, hq, hkv, d, causal, window, scale = case
+    lengths = _lengths(lengths)
     (q, k, v), (qh, kh, vh) = _inputs(lengths, hq, hkv, d, 1, torch.bfloat16, torch, cuda, scale)
     cu = oa.cu_from_lengths(lengths)
     ref = oa.varlen_attention(qh, kh, vh, cu, causal=causal, window=window, scale=scale)
@@ -157,3 +175,41 @@ def test_peaky_logits_bf16(pv_bf16, cuda, inl):
     err = np.abs(out.cpu().numpy() - ref).max()
     print(f"peaky pv_bf16={pv_bf16} max abs err={err:.3g}", flush=True)
     assert err <= (8e-3 if pv_bf16 else 2e-3)
+
+
+def test_pv_fp16_range_contract(cuda, inl):
+    """The default bf16 path runs PV in fp16 (include/inl_hip.h): a value
+    |v| >= 65520 becomes inf. Text 1 holds one key row of 70,000 at position
+    40. By default its rows that see that key are non-finite, while the
+    other texts of the batch stay within 2e-3 of the oracle. With
+    INL_ATTN_PV_BF16 every row is finite. There the weights that multiply V
+    are bf16-rounded P divided by the sum of the same rounded values: each
+    carries at most 2u relative error (u = 2^-8, bf16's unit roundoff), so
+    a row is within 2e-3 + 2^-7 * sum_j p_j |v_j| of the oracle."""
+    import torch
+    lengths, hq, hkv, d, scale = [70, 90, 33], 16, 8, 128, 128 ** -0.5
+    (q, k, v), (qh, kh, vh) = _inputs(lengths, hq, hkv, d, 7, torch.bfloat16, torch, cuda, scale)
+    cu = oa.cu_from_lengths(lengths)
+    big = int(cu[1]) + 40
+    v[big] = 70000.0
+    vh = v.float().cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(vh[big]) >= 65520)
+    ref = oa.varlen_attention(qh, kh, vh, cu, causal=True, scale=scale)
+    mag = oa.varlen_attention(qh, kh, np.abs(vh), cu, causal=True, scale=scale)
+    print("case=pv_fp16_range lengths=", lengths, flush=True)
+    out = inl.varlen_attention(q, k, v, cu.tolist(), causal=True, scale=scale, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    t1 = slice(int(cu[1]), int(cu[2]))
+    others = np.r_[int(cu[0]):int(cu[1]), int(cu[2]):int(cu[3])]
+    assert not np.isfinite(got[big:int(cu[2])]).any(), "rows that see the key must overflow in fp16 PV"
+    assert np.abs(got[others] - ref[others]).max() <= 2e-3
+    out = inl.varlen_attention(q, k, v, cu.tolist(), causal=True, scale=scale, out_dtype=torch.float32,
+                               flags=inl.ATTN_PV_BF16)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    ratio = (np.abs(got - ref) / (2e-3 + 2.0 ** -7 * mag)).max()
+    print(f"pv_bf16: worst error / bound = {ratio:.3f}", flush=True)
+    assert ratio <= 1.0
+    assert np.abs(got[t1]).max() > 1000.0  # the large key is really in play

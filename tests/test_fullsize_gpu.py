@@ -15,8 +15,8 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-CASES = ["config2_all_in_one_launch", "qwen3_2048_causal", "gemma_window512", "modernbert_local64",
-         "pplx_causal"]
+CASES = ["config2_all_in_one_launch", "qwen3_2048_causal", "gemma_window512", "gemma_full",
+         "modernbert_local64", "modernbert_global", "pplx_causal", "vision"]
 
 
 def _case(name):
@@ -27,8 +27,11 @@ def _case(name):
         "config2_all_in_one_launch": (w.qwen3_op_lengths(), 16, 8, 128, True, -1),
         "qwen3_2048_causal": ([2048] * 32, 16, 8, 128, True, -1),
         "gemma_window512": (w.uniform_lengths(32, 64, 8192), 3, 1, 256, False, 512),
+        "gemma_full": (w.uniform_lengths(32, 64, 8192), 3, 1, 256, False, -1),
         "modernbert_local64": (w.uniform_lengths(128, 32, 2048), 12, 12, 64, False, 64),
+        "modernbert_global": (w.uniform_lengths(128, 32, 2048), 12, 12, 64, False, -1),
         "pplx_causal": ([4096] * 16, 16, 2, 256, True, -1),
+        "vision": ([256] * 64, 16, 16, 64, False, -1),
     }[name]
 
 
@@ -52,20 +55,25 @@ def _expected_means(vh, lengths, causal, window):
     return out
 
 
-@pytest.mark.parametrize("name", CASES)
-def test_uniform_keys_give_visible_means(name, cuda, inl):
+F32_CASES = ["modernbert_local64", "modernbert_global", "qwen3_2048_causal"]
+
+
+@pytest.mark.parametrize("name,dtype", [(c, "bf16") for c in CASES] + [(c, "f32") for c in F32_CASES],
+                         ids=[c for c in CASES] + [c + "-f32" for c in F32_CASES])
+def test_uniform_keys_give_visible_means(name, dtype, cuda, inl):
     import torch
     lengths, hq, hkv, d, causal, window = _case(name)
     n = int(sum(lengths))
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     g = torch.Generator(device=cuda).manual_seed(7)
-    q = torch.randn(n, hq, d, generator=g, device=cuda).to(torch.bfloat16)
-    k = torch.zeros(n, hkv, d, device=cuda, dtype=torch.bfloat16)
-    v = torch.randn(n, hkv, d, generator=g, device=cuda).to(torch.bfloat16)
+    q = torch.randn(n, hq, d, generator=g, device=cuda).to(tdt)
+    k = torch.zeros(n, hkv, d, device=cuda, dtype=tdt)
+    v = torch.randn(n, hkv, d, generator=g, device=cuda).to(tdt)
     out = torch.full((n, hq, d), float("nan"), device=cuda, dtype=torch.float32)
     cu = [0]
     for t in lengths:
         cu.append(cu[-1] + int(t))
-    print(f"full-size {name}: {len(lengths)} texts, {n} tokens", flush=True)
+    print(f"full-size {name} {dtype}: {len(lengths)} texts, {n} tokens", flush=True)
     inl.varlen_attention(q, k, v, cu, causal=causal, window=window, scale=d ** -0.5, out=out)
     torch.cuda.synchronize()
     group = hq // hkv
@@ -78,3 +86,90 @@ def test_uniform_keys_give_visible_means(name, cuda, inl):
             worst = max(worst, float(np.abs(got - exp).max()))
     print(f"full-size {name}: max abs err {worst:.3g}", flush=True)
     assert worst <= 1e-3
+
+
+def _sample_rows(lengths, per_text, rng):
+    """Row indices per text: the first two, the middle, the last, and
+    ``per_text`` more at random (all of them for short texts)."""
+    rows, s = [], 0
+    for t in lengths:
+        if t <= per_text + 4:
+            pick = np.arange(t)
+        else:
+            pick = np.unique(np.concatenate([[0, 1, t // 2, t - 1], rng.integers(0, t, per_text)]))
+        rows.append(s + pick)
+        s += t
+    return rows
+
+
+def _textbook_rows(qrows, kh, vh, lengths, rows, hq, hkv, causal, window, scale):
+    """softmax(scale q.k) V over each sampled query's visible keys, f64, for
+    every query head (head h reads KV head h // (hq/hkv)). ``qrows`` maps a
+    sampled row to its f64 ``[hq, d]`` queries; ``kh``/``vh`` are the f32
+    keys and values, converted to f64 one text at a time."""
+    group = hq // hkv
+    out = {}
+    s = 0
+    for t, picks in zip(lengths, rows):
+        kt, vt = kh[s:s + t].astype(np.float64), vh[s:s + t].astype(np.float64)
+        for r in picks:
+            i = r - s
+            lo = 0 if window < 0 else max(0, i - window)
+            hi = i + 1 if causal else t
+            if window >= 0:
+                hi = min(hi, i + window + 1)
+            kk, vv = kt[lo:hi], vt[lo:hi]           # [keys, hkv, d]
+            for h in range(hq):
+                sc = kk[:, h // group] @ qrows[r][h] * scale
+                p = np.exp(sc - sc.max())
+                out[(r, h)] = (p / p.sum()) @ vv[:, h // group]
+        s += t
+    return out
+
+
+SAMPLED = [(c, "bf16") for c in ("config2_all_in_one_launch", "qwen3_2048_causal", "gemma_window512",
+                                 "gemma_full", "modernbert_local64", "modernbert_global", "pplx_causal")] + \
+          [(c, "f32") for c in ("modernbert_local64", "modernbert_global")]
+
+
+@pytest.mark.parametrize("name,dtype", SAMPLED, ids=[f"{c}-{d}" for c, d in SAMPLED])
+def test_sampled_rows_match_textbook_full_size(name, dtype, cuda, inl):
+    """Random RMS-normalised q/k and N(0,1) v at the benchmark shapes and full
+    sizes, in one launch; the first, second, middle and last query of every
+    text and 12 more at random are checked against the textbook softmax over
+    their visible keys (f64 on the host, from the same rounded inputs):
+    <= 2e-3 max-abs in bf16, <= 1e-5 in f32 (the north star's bounds)."""
+    import torch
+    lengths, hq, hkv, d, causal, window = _case(name)
+    n = int(sum(lengths))
+    scale = d ** -0.5
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    g = torch.Generator(device=cuda).manual_seed(11)
+
+    def normed(h):
+        x = torch.randn(n, h, d, generator=g, device=cuda)
+        return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6)
+
+    q = normed(hq).to(tdt)
+    k = normed(hkv).to(tdt)
+    v = torch.randn(n, hkv, d, generator=g, device=cuda).to(tdt)
+    out = torch.full((n, hq, d), float("nan"), device=cuda, dtype=torch.float32)
+    cu = [0]
+    for t in lengths:
+        cu.append(cu[-1] + int(t))
+    print(f"full-size sampled {name} {dtype}: {len(lengths)} texts, {n} tokens", flush=True)
+    inl.varlen_attention(q, k, v, cu, causal=causal, window=window, scale=scale, out=out)
+    torch.cuda.synchronize()
+    rows = _sample_rows(lengths, 12, np.random.default_rng(5))
+    flat_np = np.concatenate(rows)
+    flat = torch.from_numpy(flat_np).to(cuda)
+    qs = q[flat].float().cpu().numpy().astype(np.float64)
+    qrows = {int(r): qs[j] for j, r in enumerate(flat_np)}
+    kh, vh = k.float().cpu().numpy(), v.float().cpu().numpy()
+    got = out[flat].cpu().numpy()
+    want = _textbook_rows(qrows, kh, vh, lengths, rows, hq, hkv, causal, window, scale)
+    pos = {int(r): j for j, r in enumerate(flat_np)}
+    worst = max(float(np.abs(got[pos[r], h] - ref).max()) for (r, h), ref in want.items())
+    print(f"full-size sampled {name} {dtype}: {len(pos)} rows x {hq} heads, max abs err {worst:.3g}", flush=True)
+    assert np.isfinite(got).all()
+    assert worst <= (2e-3 if dtype == "bf16" else 1e-5)

@@ -73,3 +73,69 @@ def test_pool_last_and_mean_full_size(cuda, inl):
     print(f"full-size pooling: last max abs err {e_last:.3g}, mean-of-constant err {e_mean:.3g}", flush=True)
     assert e_last <= 1e-5
     assert e_mean <= 1e-5 * 4
+
+
+def test_splade_full_vocab_config4_planted_maxima(cuda, inl):
+    """SPLADE pooling at config 4's full size: 128 texts of U[32,2048] tokens,
+    every token but the first (the prefix) speaking, 135,764 speaking rows of
+    f32 logits over the 50,002-term vocabulary (27.2 GB), folded onto 36,282
+    canonical terms, shift 10, masked ids 50000/50001, a random bias in
+    [-1, 1] (crates/inl-sparse/src/modernbert.rs:806-907).
+
+    Planted maxima make the answer known exactly: the background logits lie
+    in [-8, shift - 2], so with the bias every background term finishes at 0.
+    Each row gets 64 planted terms (some masked, some folded onto the same
+    canonical term), each planted at 3 of its row's positions with the
+    largest value above the shift. The expected output is the oracle's
+    finish and fold of the row maxima; values within 1e-6 and the active-term
+    sets bit-exact, as the north star asks of f32 mode."""
+    import torch
+    from inl_hip import workloads
+    from oracle import pooling as opl
+    lens = workloads.uniform_lengths(128, 32, 2048)
+    speak = np.array([t - 1 for t in lens], dtype=np.int64)
+    offs = np.concatenate([[0], np.cumsum(speak)]).astype(np.int32)
+    n_rows, vocab, terms, shift = len(lens), 50002, 36282, 10.0
+    masked = [50000, 50001]
+    rng = np.random.default_rng(21)
+    canonical = np.concatenate([rng.permutation(terms), rng.integers(0, terms, vocab - terms)]).astype(np.int32)
+    bias = rng.uniform(-1.0, 1.0, vocab).astype(np.float32)
+    S = int(offs[-1])
+    print(f"full-size splade: {n_rows} rows, {S} speaking positions x {vocab} terms", flush=True)
+    logits = torch.empty((S, vocab), dtype=torch.float32, device=cuda)
+    logits.uniform_(-8.0, shift - 2.0, generator=torch.Generator(device=cuda).manual_seed(5))
+    m = np.full((n_rows, vocab), shift - 2.0, dtype=np.float32)   # finishes at 0 like the background
+    pos_all, term_all, val_all = [], [], []
+    for r in range(n_rows):
+        t_pick = rng.choice(vocab, size=64, replace=False)
+        t_pick[:2] = masked                                # planted but masked
+        t_pick[2] = 0
+        t_pick[3] = int(np.nonzero(canonical == canonical[0])[0][-1])  # shares term 0's canonical id
+        t_pick = np.unique(t_pick)
+        for t in t_pick:
+            p = rng.choice(np.arange(offs[r], offs[r + 1]), size=min(3, int(speak[r])), replace=False)
+            vals = (shift + rng.uniform(0.5, 6.0, size=len(p))).astype(np.float32)
+            pos_all.append(p)
+            term_all.append(np.full(len(p), t))
+            val_all.append(vals)
+            m[r, t] = vals.max()
+    pi = torch.from_numpy(np.concatenate(pos_all)).to(cuda)
+    ti = torch.from_numpy(np.concatenate(term_all)).to(cuda)
+    logits[pi, ti] = torch.from_numpy(np.concatenate(val_all)).to(cuda)
+    out = inl.pool_splade(logits, torch.from_numpy(offs).to(cuda), bias=torch.from_numpy(bias).to(cuda),
+                          shift=shift, masked_ids=masked, canonical=torch.from_numpy(canonical).to(cuda),
+                          out_dim=terms)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    del logits
+    want = opl.splade_fold(opl.splade_finish(m, bias, shift, masked), canonical)
+    err = float(np.abs(got - want).max())
+    n_active = 0
+    for r in range(n_rows):
+        gi, _ = opl.sparse_from_pairs(got[r])
+        wi, _ = opl.sparse_from_pairs(want[r])
+        assert np.array_equal(gi, wi), f"row {r}: active sets differ"
+        n_active += len(wi)
+    print(f"full-size splade: max abs err {err:.3g}, {n_active} active terms", flush=True)
+    assert err <= 1e-6
+    assert n_active >= n_rows * 50
