@@ -846,10 +846,10 @@ int check_ptrs(const void* q, const void* k, const void* v, const void* out, int
 namespace inl {
 namespace {
 
-// Upload a schedule into device memory `buf` (a caller workspace) and
-// launch. The schedule is copied from ordinary (pageable) host memory:
-// hipMemcpyAsync takes the data before it returns, so nothing pinned is
-// allocated; the copy orders behind the stream's earlier work.
+// Upload a schedule into device memory `buf` (a caller workspace or the
+// static scratch) and launch. The schedule is copied from ordinary (pageable)
+// host memory: hipMemcpyAsync takes the data before it returns, so nothing
+// pinned is allocated; the copy orders behind the stream's earlier work.
 int launch_one_shot(const inl_attn_desc* desc, const Schedule& s, void* buf, const void* q, const void* k,
                     const void* v, void* out, hipStream_t stream) {
   int rc = ensure_lds_attr(s.cfg);
@@ -959,6 +959,67 @@ extern "C" int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q, con
     return fail(INL_E_INVALID, "attention: workspace is NULL or smaller than inl_attn_workspace_size()");
   if (!aligned16(workspace)) return fail(INL_E_INVALID, "attention: workspace must be 16-byte aligned");
   return launch_one_shot(desc, s, workspace, q, k, v, out, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free one-shot form: the schedule goes into `scratch`, a static
+// device array of the library, instead of a caller workspace.
+// ---------------------------------------------------------------------------
+
+namespace inl {
+namespace {
+
+// Each GPU the library runs on holds its own copy until the process ends.
+// Host code never uses this name as an address: it is a host-side stand-in.
+// The device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) char scratch[INL_ATTN_STATIC_SCHEDULE_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The calling thread's current device's copy of `scratch`, looked up on the
+// first call on that device (with that device current).
+int scratch_on_current_device(void** ptr) {
+  int dev = 0;
+  INL_HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(INL_E_UNSUPPORTED, "attention: device ordinal beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    INL_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(INL_E_HIP, "attention: hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return INL_OK;
+}
+
+}  // namespace
+}  // namespace inl
+
+extern "C" int inl_attn_varlen_fwd_static(const inl_attn_desc* desc, const void* q, const void* k,
+                                          const void* v, void* out, void* stream) {
+  using namespace inl;
+  int64_t total = 0;
+  int rc = validate_desc(desc, &total);
+  if (rc) return rc;
+  rc = check_ptrs(q, k, v, out, total);
+  if (rc) return rc;
+  Schedule s;
+  rc = build_schedule(desc, &s);
+  if (rc) return rc;
+  const size_t need = s.bytes();
+  if (need == 0) return INL_OK;
+  if (need > INL_ATTN_STATIC_SCHEDULE_BYTES)
+    return fail(INL_E_INVALID, "attention: the batch's schedule needs " + std::to_string(need) +
+                                   " bytes, more than the static buffer's " +
+                                   std::to_string((size_t)INL_ATTN_STATIC_SCHEDULE_BYTES) +
+                                   "; split the batch or use inl_attn_varlen_fwd with a workspace");
+  void* buf = nullptr;
+  rc = scratch_on_current_device(&buf);
+  if (rc) return rc;
+  return launch_one_shot(desc, s, buf, q, k, v, out, (hipStream_t)stream);
 }
 
 extern "C" int inl_attn_kernel_name(const inl_attn_desc* desc, const char** name) {

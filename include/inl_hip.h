@@ -133,6 +133,23 @@ int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q,
                         const void* k, const void* v, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free one-shot form. It has no counterpart in the reference: it
+ * is for callers that cannot allocate device memory per call (tight serving
+ * loops, harnesses that forbid hipMalloc). It runs the same kernels as
+ * inl_attn_varlen_fwd, with the same results, but keeps the schedule in a
+ * static device buffer of the library, INL_ATTN_STATIC_SCHEDULE_BYTES per
+ * GPU (held by each GPU the library runs on until the process ends), so it
+ * takes no workspace and calls no allocator. A batch whose schedule is
+ * larger (about 200k units of work: far beyond any batch an engine plans)
+ * fails with INL_E_INVALID. All calls on one GPU share that buffer: calls
+ * in order on one stream are safe, while calls that overlap on one GPU (two
+ * streams, or two host threads on different streams) race and must be
+ * serialised by the caller. */
+#define INL_ATTN_STATIC_SCHEDULE_BYTES (4u << 20)
+int inl_attn_varlen_fwd_static(const inl_attn_desc* desc, const void* q,
+                               const void* k, const void* v, void* out,
+                               void* stream);
+
 /* Host only: the name of the kernel a plan for `desc` launches (a static
  * string, e.g. "attn_pp_kernel<128, 64>"), for reporting and tests. The
  * bf16 fast kernels address each text's rows with 32-bit offsets; a text
