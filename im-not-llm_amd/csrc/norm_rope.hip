@@ -1,12 +1,12 @@
 // Fused per-head RMSNorm + RoPE prologue for packed encoder rows (gfx950).
 //
-// One (token, head) row of head_dim elements is handled by G = head_dim / 8
-// lanes, each owning 8 contiguous elements (one 16-byte bf16 chunk): the
+// A token is handled by G = head_dim / 8 lanes, each owning 8 contiguous
+// elements (one 16-byte bf16 chunk) of every head row of that token: the
 // sum of squares is reduced over the G lanes with shuffles, and a rotation
 // partner (element i + half of a half-split pair) lives in lane j +/- half/8
-// and is exchanged with one shuffle per element. HBM-bound: one read of x,
-// one write of y; weights and cos/sin tables are shared by every row and
-// stay in cache.
+// and is exchanged with one shuffle per element. The weight and the token's
+// cos/sin are loaded once per token, not once per head. HBM-bound: one read
+// of x, one write of y.
 //
 // Replaces, per layer, the reference's q/k(/v) RMSNorm and RoPE kernels
 // (crates/inl-text/src/qwen3/mod.rs:236-249, gemma2.rs:389-410,
@@ -31,7 +31,7 @@ struct NormRopeParams {
   const float* sin;
   const float* cos2;
   const float* sin2;
-  int64_t n_rows;           // tokens * heads
+  int64_t n_tokens;
   int32_t heads;
   int32_t head_dim;
   int64_t x_stride, y_stride;  // elements between token rows
@@ -77,63 +77,44 @@ __device__ __forceinline__ void store8(char* p, const float (&v)[8]) {
   }
 }
 
+// A group of G = head_dim / 8 lanes owns one token: each lane holds 8
+// elements of a head row. The token's norm weight, table row and the lane's
+// cos/sin columns are loaded once per group of HB = 4 heads of the token
+// (each lane group owns one (token, head chunk)), so per (token, head) x is
+// read and y written and the tables cost a quarter of that in cache reads;
+// the 4 loads of a lane go out together. Every lane of a wave runs the head
+// step the same number of times (the shuffles need all of them).
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
+  constexpr int HB = 4;                          // heads per step
   const int G = p.head_dim >> 3;                 // lanes per row (power of two <= 64)
   const int lane = threadIdx.x & 63;
   const int j = lane & (G - 1);                  // chunk of the row this lane owns
-  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / G;
-  const bool valid = row < p.n_rows;             // whole groups are valid or not
-  const int64_t tok = valid ? row / p.heads : 0;
-  const int head = valid ? (int)(row - tok * p.heads) : 0;
+  // lane group -> (token, chunk of HB heads)
+  const uint32_t chunks = ((uint32_t)p.heads + HB - 1) / HB;
+  const uint32_t grp = blockIdx.x * (256u / (uint32_t)G) + threadIdx.x / (uint32_t)G;
+  const uint32_t tok = grp / chunks;
+  const int hfirst = (int)(grp - tok * chunks) * HB;
+  const bool valid = tok < (uint32_t)p.n_tokens;
+  const int heads = min(p.heads, hfirst + HB);
 
-  float v[8];
-  if (valid) load8<TI>(p.x + (tok * p.x_stride + (int64_t)head * p.head_dim + 8 * j) * (int64_t)sizeof(TI), v);
-  else
+  // ---- per-token constants ----
+  float w[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+  for (int e = 0; e < 8; ++e) w[e] = 1.f;
+  if (p.norm && p.w) load8<TI>(p.w + 8 * j * (int)sizeof(TI), w);
 
-  if (p.norm) {
-    float ss = 0.f;
+  // rope geometry: `mode` 0 = none for this lane, 1 = pairs (e, e + 4) inside
+  // the lane (rotary_dim 8), 2 = half-split with the partner lane
+  int mode = 0, partner = lane;
+  bool first = true;
+  float c[8], sn[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-    for (int m = G >> 1; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
-    const float inv = 1.0f / sqrtf(ss / (float)p.head_dim + p.eps);
-    float w[8];
-    if (p.w) load8<TI>(p.w + 8 * j * (int)sizeof(TI), w);
-    else
-#pragma unroll
-      for (int e = 0; e < 8; ++e) w[e] = 1.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      v[e] = v[e] * inv * w[e];
-      if (p.round_norm && sizeof(TO) == 2) v[e] = round_bf16(v[e]);
-    }
-  }
-
+  for (int e = 0; e < 8; ++e) { c[e] = 1.f; sn[e] = 0.f; }
+  bool bad_pos = false;
   if (p.rotary_dim == 8 && p.sections == 1) {
-    // Both halves of the rotated section sit in chunk 0: pairs (e, e + 4)
-    // rotate inside the lane, by table column e (4 columns).
-    if (j == 0 && valid) {
-      const int32_t pos = p.rows[tok];
-      if (pos < 0 || pos >= p.table_rows) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = __builtin_nanf("");
-      } else {
-        const f32x4 c = *reinterpret_cast<const f32x4*>(p.cos + (int64_t)pos * 4);
-        const f32x4 s = *reinterpret_cast<const f32x4*>(p.sin + (int64_t)pos * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float ce = c[e], se = s[e];
-          if (p.round_tables) { ce = round_bf16(ce); se = round_bf16(se); }
-          const float a = v[e], b = v[e + 4];
-          v[e] = a * ce - b * se;
-          v[e + 4] = b * ce + a * se;
-        }
-      }
-    }
+    mode = j == 0 ? 1 : 0;
   } else if (p.rotary_dim > 0) {
-    // Geometry of the half-split this lane belongs to.
     int sec_lanes, sec0;  // lanes per rotated section, first lane of it
     if (p.sections == 2) {
       sec_lanes = G >> 1;
@@ -144,36 +125,88 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
     }
     const int half_lanes = sec_lanes >> 1;
     const int jj = j - sec0;                         // chunk inside the section
-    const bool rotated = jj >= 0 && jj < sec_lanes;  // pass-through chunks are not
-    const bool first = jj < half_lanes;
-    const int partner = lane + (first ? half_lanes : -half_lanes);
-    float pv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) pv[e] = __shfl(v[e], rotated ? partner : lane, 64);
-    if (rotated && valid) {
-      const int32_t pos = p.rows[tok];
-      const int width = half_lanes * 8;              // table columns
-      const float* ct = (p.sections == 2 && !(j < (G >> 1))) ? p.cos2 : p.cos;
-      const float* st = (p.sections == 2 && !(j < (G >> 1))) ? p.sin2 : p.sin;
-      if (pos < 0 || pos >= p.table_rows) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = __builtin_nanf("");
-      } else {
-        const int col = 8 * (first ? jj : jj - half_lanes);
-        float c[8], s[8];
-        load8<float>(reinterpret_cast<const char*>(ct + (int64_t)pos * width + col), c);
-        load8<float>(reinterpret_cast<const char*>(st + (int64_t)pos * width + col), s);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float ce = c[e], se = s[e];
-          if (p.round_tables) { ce = round_bf16(ce); se = round_bf16(se); }
-          v[e] = first ? (v[e] * ce - pv[e] * se) : (v[e] * ce + pv[e] * se);
-        }
-      }
+    if (jj >= 0 && jj < sec_lanes) {
+      mode = 2;
+      first = jj < half_lanes;
+      partner = lane + (first ? half_lanes : -half_lanes);
     }
   }
+  if (mode != 0 && valid) {
+    const int32_t pos = p.rows[tok];
+    if (pos < 0 || pos >= p.table_rows) {
+      bad_pos = true;
+    } else if (mode == 1) {
+      const f32x4 c4 = *reinterpret_cast<const f32x4*>(p.cos + (int64_t)pos * 4);
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(p.sin + (int64_t)pos * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { c[e] = c4[e]; sn[e] = s4[e]; }
+    } else {
+      int sec_lanes = p.sections == 2 ? G >> 1 : p.rotary_dim >> 3;
+      const int half_lanes = sec_lanes >> 1;
+      const int width = half_lanes * 8;              // table columns
+      const bool second_sec = p.sections == 2 && !(j < (G >> 1));
+      const float* ct = second_sec ? p.cos2 : p.cos;
+      const float* st = second_sec ? p.sin2 : p.sin;
+      const int jj = j - (second_sec ? (G >> 1) : 0);
+      const int col = 8 * (first ? jj : jj - half_lanes);
+      load8<float>(reinterpret_cast<const char*>(ct + (int64_t)pos * width + col), c);
+      load8<float>(reinterpret_cast<const char*>(st + (int64_t)pos * width + col), sn);
+    }
+    if (p.round_tables)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { c[e] = round_bf16(c[e]); sn[e] = round_bf16(sn[e]); }
+  }
 
-  if (valid) store8<TO>(p.y + (tok * p.y_stride + (int64_t)head * p.head_dim + 8 * j) * (int64_t)sizeof(TO), v);
+  const char* xt = p.x + ((int64_t)tok * p.x_stride + 8 * j) * (int64_t)sizeof(TI);
+  char* yt = p.y + ((int64_t)tok * p.y_stride + 8 * j) * (int64_t)sizeof(TO);
+  const int64_t hstep_x = (int64_t)p.head_dim * (int64_t)sizeof(TI);
+  const int64_t hstep_y = (int64_t)p.head_dim * (int64_t)sizeof(TO);
+  for (int h0 = hfirst; h0 < heads; h0 += HB) {   // one step
+    float v[HB][8];
+#pragma unroll
+    for (int i = 0; i < HB; ++i) {
+      if (valid && h0 + i < heads) load8<TI>(xt + (h0 + i) * hstep_x, v[i]);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < HB; ++i) {
+      if (p.norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+        for (int m = G >> 1; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float inv = 1.0f / sqrtf(ss / (float)p.head_dim + p.eps);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v[i][e] = v[i][e] * inv * w[e];
+          if (p.round_norm && sizeof(TO) == 2) v[i][e] = round_bf16(v[i][e]);
+        }
+      }
+      if (mode == 1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = v[i][e], b = v[i][e + 4];
+          v[i][e] = a * c[e] - b * sn[e];
+          v[i][e + 4] = b * c[e] + a * sn[e];
+        }
+      }
+      if (p.rotary_dim > 0 && !(p.rotary_dim == 8 && p.sections == 1)) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = __shfl(v[i][e], partner, 64);
+        if (mode == 2)
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            v[i][e] = first ? (v[i][e] * c[e] - pv[e] * sn[e]) : (v[i][e] * c[e] + pv[e] * sn[e]);
+      }
+      if (bad_pos)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = __builtin_nanf("");
+      if (valid && h0 + i < heads) store8<TO>(yt + (h0 + i) * hstep_y, v[i]);
+    }
+  }
 }
 
 }  // namespace
@@ -227,7 +260,7 @@ extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, voi
   p.sin = sin;
   p.cos2 = cos2;
   p.sin2 = sin2;
-  p.n_rows = d->n_tokens * d->heads;
+  p.n_tokens = d->n_tokens;
   p.heads = d->heads;
   p.head_dim = hd;
   p.x_stride = xs;
@@ -241,9 +274,11 @@ extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, voi
   p.round_norm = d->round_norm;
 
   const int G = hd >> 3;
-  const int64_t threads = p.n_rows * G;
-  const int64_t blocks = (threads + 255) / 256;
-  if (blocks > 0x7fffffff) return fail(INL_E_UNSUPPORTED, "norm_rope: too many rows");
+  const int64_t groups_per_block = 256 / G;
+  const int64_t groups = d->n_tokens * ((d->heads + 3) / 4);   // (token, 4-head chunk)
+  if (groups + groups_per_block >= ((int64_t)1 << 31))
+    return fail(INL_E_UNSUPPORTED, "norm_rope: tokens x head chunks must stay below 2^31");
+  const int64_t blocks = (groups + groups_per_block - 1) / groups_per_block;
   hipStream_t st = (hipStream_t)stream;
   if (d->dtype == INL_BF16 && d->out_dtype == INL_BF16)
     hipLaunchKernelGGL((norm_rope_kernel<bf16, bf16>), dim3((unsigned)blocks), dim3(256), 0, st, p);

@@ -71,7 +71,68 @@ __global__ __launch_bounds__(256) void pool_last_kernel(const char* hidden, int6
   for (int i = threadIdx.x; i < h; i += blockDim.x) o[i] = o[i] / n;
 }
 
-// ---- mean: one block per (text, 64-column slice); 4 row phases ----
+// ---- mean, vector form: one block of 1024 lanes per (text, column slice) ----
+// 16 lanes cover a slice of 16 * VW columns of a row with one 16-byte load
+// each (VW = 16 / sizeof(T)); the 64 lane rows walk the text's rows 64 apart,
+// four rows per step, so each lane has four loads in flight. The 64 partial
+// sums of a column are then added in a fixed order through LDS: the result
+// does not depend on timing (no atomics).
+template <typename T>
+__global__ __launch_bounds__(1024) void pool_mean_vec_kernel(const char* hidden, int64_t stride, const int32_t* cu,
+                                                             int32_t h, float* out) {
+  constexpr int VW = 16 / sizeof(T);
+  constexpr int COLS = 16 * VW;
+  __shared__ float part[64][COLS];
+  const int b = blockIdx.y;
+  const int l = threadIdx.x & 15;
+  const int rg = threadIdx.x >> 4;
+  const int c0 = blockIdx.x * COLS + l * VW;
+  const int32_t s0 = cu[b], s1 = cu[b + 1];
+  float acc[VW];
+#pragma unroll
+  for (int e = 0; e < VW; ++e) acc[e] = 0.f;
+  auto add = [&](const u32x4& w) __attribute__((always_inline)) {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[2 * q] += __builtin_bit_cast(float, w[q] << 16);
+        acc[2 * q + 1] += __builtin_bit_cast(float, w[q] & 0xffff0000u);
+      }
+    } else {
+      // cast the whole vector: a bit_cast of one element lvalue of a vector
+      // type reads element 0 here
+      const f32x4 f = __builtin_bit_cast(f32x4, w);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] += f[q];
+    }
+  };
+  if (c0 < h) {
+    const char* base = hidden + (int64_t)c0 * (int64_t)sizeof(T);
+    const int64_t rstep = stride * (int64_t)sizeof(T);
+    int32_t r = s0 + rg;
+    for (; r + 3 * 64 < s1; r += 4 * 64) {
+      u32x4 w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = *reinterpret_cast<const u32x4*>(base + (int64_t)(r + 64 * k) * rstep);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) add(w[k]);
+    }
+    for (; r < s1; r += 64) add(*reinterpret_cast<const u32x4*>(base + (int64_t)r * rstep));
+  }
+#pragma unroll
+  for (int e = 0; e < VW; ++e) part[rg][l * VW + e] = acc[e];
+  __syncthreads();
+  if (threadIdx.x < COLS) {
+    const int c = blockIdx.x * COLS + threadIdx.x;
+    float sum = 0.f;
+    for (int i = 0; i < 64; ++i) sum += part[i][threadIdx.x];
+    const int32_t n = s1 - s0;
+    if (c < h) out[(int64_t)b * h + c] = n > 0 ? sum / (float)n : 0.f;
+  }
+}
+
+// ---- mean, generic form (rows or columns not 16-byte aligned): one block
+// per (text, 64-column slice); 4 row phases ----
 template <typename T>
 __global__ __launch_bounds__(256) void pool_mean_kernel(const char* hidden, int64_t stride, const int32_t* cu,
                                                         int32_t h, float* out) {
@@ -196,11 +257,25 @@ extern "C" int inl_pool_mean_fwd(int32_t n_texts, const int32_t* cu, int32_t hid
   if (!cu || !hidden || !pooled || rs < hidden_dim) return fail(INL_E_INVALID, "pool_mean: NULL pointer or bad stride");
   if (n_texts > 65535) return fail(INL_E_UNSUPPORTED, "pool_mean: more than 65535 texts in one call");
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid((hidden_dim + 63) / 64, n_texts);
-  if (dtype == INL_BF16)
-    hipLaunchKernelGGL(pool_mean_kernel<bf16>, grid, dim3(256), 0, st, (const char*)hidden, rs, cu, hidden_dim, pooled);
-  else
-    hipLaunchKernelGGL(pool_mean_kernel<float>, grid, dim3(256), 0, st, (const char*)hidden, rs, cu, hidden_dim, pooled);
+  const int es = dtype_size(dtype);
+  const bool vec = ((uintptr_t)hidden % 16 == 0) && (rs * es) % 16 == 0 && (hidden_dim * es) % 16 == 0;
+  if (vec) {
+    dim3 grid((hidden_dim + 16 * (16 / es) - 1) / (16 * (16 / es)), n_texts);
+    if (dtype == INL_BF16)
+      hipLaunchKernelGGL(pool_mean_vec_kernel<bf16>, grid, dim3(1024), 0, st, (const char*)hidden, rs, cu,
+                         hidden_dim, pooled);
+    else
+      hipLaunchKernelGGL(pool_mean_vec_kernel<float>, grid, dim3(1024), 0, st, (const char*)hidden, rs, cu,
+                         hidden_dim, pooled);
+  } else {
+    dim3 grid((hidden_dim + 63) / 64, n_texts);
+    if (dtype == INL_BF16)
+      hipLaunchKernelGGL(pool_mean_kernel<bf16>, grid, dim3(256), 0, st, (const char*)hidden, rs, cu, hidden_dim,
+                         pooled);
+    else
+      hipLaunchKernelGGL(pool_mean_kernel<float>, grid, dim3(256), 0, st, (const char*)hidden, rs, cu, hidden_dim,
+                         pooled);
+  }
   INL_HIP_TRY(hipGetLastError());
   if (normalize) {
     hipLaunchKernelGGL(l2_kernel, dim3(n_texts), dim3(256), 0, st, pooled, (int64_t)hidden_dim, pooled,

@@ -66,6 +66,32 @@ def test_mean_and_matryoshka(dtype, cuda, inl):
         assert np.abs(t.cpu().numpy() - want).max() <= 1e-6
 
 
+@pytest.mark.parametrize("h,dtype,sliced", [(104, "bf16", False), (100, "f32", False), (766, "bf16", True),
+                                            (1024, "bf16", False)])
+def test_mean_shapes_and_determinism(h, dtype, sliced, cuda, inl):
+    """The vector kernel (16-byte rows: partial last column slice, f32 and
+    bf16) and the generic one (a column slice of a wider buffer, rows not
+    16-byte multiples), each within 2e-6 of the oracle on ragged texts,
+    including a long one and an empty one; the vector kernel's result is
+    bit-identical across calls (fixed summation order, no atomics)."""
+    import torch
+    lengths = [5, 0, 3000, 1, 257, 64]
+    rng = np.random.default_rng(8)
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    width = h + 2 if sliced else h
+    xt = torch.from_numpy(rng.standard_normal((sum(lengths), width)).astype(np.float32)).to(cuda).to(td)
+    if sliced:
+        xt = xt[:, 1:h + 1]
+    xh = xt.float().cpu().numpy().astype(np.float64)
+    cu = _cu(lengths, torch, cuda)
+    a = inl.pool_mean(xt, cu)
+    b = inl.pool_mean(xt, cu)
+    torch.cuda.synchronize()
+    ref = opl.mean_pool(xh, oa.cu_from_lengths(lengths))
+    assert np.abs(a.cpu().numpy() - ref).max() <= 2e-6
+    assert torch.equal(a, b)
+
+
 def _splade_gpu(inl, torch, dev, logits, rows, prefix, vocab, **kw):
     """Gather speaking positions on the host (as the reference's Speakers
     index does), then pool on the GPU."""
