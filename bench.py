@@ -28,7 +28,10 @@ Other attention workloads (--workload): gemma_window, gemma_full,
 modernbert_local, modernbert_global, vision, pplx_causal, qwen3_2048,
 qwen3_2048_full - reported the same way. Op workloads (--workload norm_rope,
 pool_last, pool_mean, splade) time the prologue and epilogue kernels at
-their configurations' full sizes against the 8 TB/s HBM roofline.
+their configurations' full sizes against the 8 TB/s HBM roofline. The
+end-to-end workloads (--workload qwen3_e2e, f32 as configuration 1, and
+qwen3_e2e_bf16) time a whole Qwen3-0.6B encode of 8 texts (778 tokens) and
+report encoded tokens/s, with the numpy f32 forward as the CPU baseline.
 """
 from __future__ import annotations
 
@@ -183,6 +186,102 @@ def roofline(tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch):
 
 
 OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade")
+E2E_WORKLOADS = ("qwen3_e2e", "qwen3_e2e_bf16")
+PEAK_F32_TFLOPS = 157.3     # dense fp32 matrix peak
+
+
+def e2e_cpu_baseline(weights, shape, ids, cu, seconds):
+    """The oracle's numpy Qwen3 forward (oracle/qwen3.py) in f32 on the host
+    cores, over the same weights and texts, repeated until `seconds` of work
+    (at least one encode). BLAS threads: all the process is given."""
+    import numpy as np
+    from oracle import qwen3 as oq
+    cfg = oq.Qwen3Config(vocab=shape.vocab, hidden=shape.hidden, intermediate=shape.intermediate,
+                         layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads,
+                         head_dim=shape.head_dim, eps=shape.eps, theta=shape.theta)
+    host = {k: v.float().cpu().numpy() for k, v in weights.items()}
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
+    except Exception:
+        cores = os.cpu_count() or 1
+    spent, runs = 0.0, 0
+    while spent < seconds or runs == 0:
+        t0 = time.perf_counter()
+        oq.encode(host, cfg, ids, cu, dtype=np.float32)
+        spent += time.perf_counter() - t0
+        runs += 1
+    tokens = int(cu[-1]) * runs
+    return {"value": round(tokens / spent, 1), "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": (f"{runs} encodes of the same {len(cu) - 1} texts ({int(cu[-1])} tokens each) through "
+                       f"oracle/qwen3.py (numpy f32 forward: BLAS GEMMs, per-text attention), {spent:.2f} s")}
+
+
+def e2e_main(args):
+    """Configuration 1 end to end: the Qwen3-0.6B-architecture encoder on 8
+    texts of U[16, 256] tokens (778), embed -> 28 layers -> last-token pooling
+    -> L2, f32 or bf16; one step = one encode."""
+    import numpy as np
+    import torch
+    import inl_hip
+    from inl_hip import workloads as w
+    dev = torch.device("cuda:0")
+    bf16 = args.workload.endswith("bf16")
+    td = torch.bfloat16 if bf16 else torch.float32
+    shape = w.Qwen3Shape()
+    lengths = w.uniform_lengths(8, 16, 256)
+    cu = np.asarray(w.cu_seqlens(lengths))
+    ids = np.random.default_rng(0).integers(0, shape.vocab, int(cu[-1])).astype(np.int32)
+    weights = w.qwen3_random_weights(shape, torch, dev, td, seed=0)
+    enc = inl_hip.Qwen3Encoder(shape, weights, max_positions=256)
+    out = torch.empty((len(lengths), shape.hidden), dtype=torch.float32, device=dev)
+    ws = torch.empty(enc.workspace_bytes(cu.tolist()) + 256, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    tokens = int(cu[-1])
+    q_out, kv_out = shape.heads * shape.head_dim, shape.kv_heads * shape.head_dim
+    per_token = 2 * (shape.hidden * (q_out + 2 * kv_out) + q_out * shape.hidden + 3 * shape.hidden * shape.intermediate)
+    flops = shape.layers * (tokens * per_token + inl_hip.attention_flops(lengths, shape.heads, shape.head_dim, True))
+    label = (f"config1: Qwen3-Embedding-0.6B-architecture encoder end to end ({'bf16' if bf16 else 'f32'}): 28 layers, "
+             f"hidden 1024, 16 Q / 8 KV heads x 128, RoPE theta 1e6, last-token pooling, L2; 8 texts U[16,256] "
+             f"= {tokens} tokens, random ids in [0,151669), random-init weights")
+    log(f"workload: {label}; {flops / 1e12:.4f} TFLOP per encode")
+
+    def step(evs=None):
+        if evs is not None:
+            evs[0][0].record(stream)
+        enc.encode(ids, cu.tolist(), out=out, workspace=ws, stream=stream)
+        if evs is not None:
+            evs[0][1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    avg_ms = timed_launches(torch, step, 1, args.steps)
+    peak = PEAK_BF16_TFLOPS if bf16 else PEAK_F32_TFLOPS
+    ach = flops / (avg_ms * 1e-3) / 1e12
+    result = {
+        "metric": METRIC, "value": round(tokens * args.steps / wall, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if bf16 else "f32",
+        "data": "synthetic (random token ids, seeded random-init weights; no checkpoint)",
+        "config": {"workload": label, "tokens_per_step": tokens, "texts": len(lengths),
+                   "tflop_per_step": round(flops / 1e12, 6),
+                   "value_is": "end-to-end encoded tokens/s (embed, 28 layers, pooling, L2 per step)"},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(ach / peak, 4), "traffic": None,
+                     "kernel": "whole encode (hipBLASLt GEMMs, attention, prologue, norms, SwiGLU, pooling)",
+                     "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"flop": flops}},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = e2e_cpu_baseline(weights, shape, ids, cu, args.cpu_seconds)
+    enc.close()
+    print(json.dumps(result), flush=True)
 
 
 def op_workload(name, torch, inl_hip, dev):
@@ -366,6 +465,9 @@ def main():
 
     if args.workload in OP_WORKLOADS:
         op_main(args)
+        return
+    if args.workload in E2E_WORKLOADS:
+        e2e_main(args)
         return
 
     import torch

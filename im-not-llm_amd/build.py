@@ -31,7 +31,10 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", f"-I{INCLUDE}",
 ]
-LINK_FLAGS = [f"--offload-arch={ARCH}", "-shared", "-fPIC"]
+# hipBLASLt (the encoder's plain GEMMs). When torch is loaded first, its
+# bundled copy of the same soname is the one bound.
+LINK_FLAGS = [f"--offload-arch={ARCH}", "-shared", "-fPIC", "-L/opt/rocm/lib", "-lhipblaslt",
+              "-Wl,-rpath,/opt/rocm/lib"]
 
 
 # Per-source flags. attn_wide.hip (head_dim 256, one wave per SIMD, ~450 of

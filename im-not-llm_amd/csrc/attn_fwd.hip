@@ -867,6 +867,7 @@ struct inl_attn_plan {
   inl_attn_desc desc;     // cu_seqlens_host and seq_starts_host are not kept
   inl::Schedule sched;    // also kept on the host for inspection
   void* d_sched = nullptr;
+  bool owns_sched = true; // false: d_sched is the caller's workspace
   int64_t total_tokens = 0;
 };
 
@@ -898,10 +899,44 @@ extern "C" int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** p
   return INL_OK;
 }
 
+extern "C" int inl_attn_plan_create_in(const inl_attn_desc* desc, void* workspace, size_t workspace_bytes,
+                                       void* stream, inl_attn_plan** plan) {
+  using namespace inl;
+  if (!plan) return fail(INL_E_INVALID, "attention: plan out-pointer is NULL");
+  *plan = nullptr;
+  int64_t total = 0;
+  int rc = validate_desc(desc, &total);
+  if (rc) return rc;
+  inl_attn_plan* pl = new (std::nothrow) inl_attn_plan();
+  if (!pl) return fail(INL_E_NOMEM, "attention: host allocation failed");
+  pl->desc = *desc;
+  pl->desc.cu_seqlens_host = nullptr;
+  pl->desc.seq_starts_host = nullptr;
+  pl->total_tokens = total;
+  pl->owns_sched = false;
+  rc = build_schedule(desc, &pl->sched);
+  if (!rc) rc = ensure_lds_attr(pl->sched.cfg);
+  const std::vector<char> blob = rc ? std::vector<char>() : pl->sched.pack();
+  if (!rc && !blob.empty()) {
+    if (!workspace || workspace_bytes < blob.size())
+      rc = fail(INL_E_INVALID, "attention: workspace is NULL or smaller than inl_attn_workspace_size()");
+    else if (!aligned16(workspace))
+      rc = fail(INL_E_INVALID, "attention: workspace must be 16-byte aligned");
+    else {
+      hipError_t e = hipMemcpyAsync(workspace, blob.data(), blob.size(), hipMemcpyHostToDevice, (hipStream_t)stream);
+      if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(plan)");
+      pl->d_sched = workspace;
+    }
+  }
+  if (rc) { delete pl; return rc; }
+  *plan = pl;
+  return INL_OK;
+}
+
 extern "C" int inl_attn_plan_destroy(inl_attn_plan* plan) {
   if (!plan) return INL_OK;
   int rc = INL_OK;
-  if (plan->d_sched) {
+  if (plan->d_sched && plan->owns_sched) {
     hipError_t e = hipFree(plan->d_sched);
     if (e != hipSuccess) rc = inl::hip_fail(e, "hipFree(plan)");
   }

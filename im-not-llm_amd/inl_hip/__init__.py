@@ -486,3 +486,180 @@ def pool_splade(logits, offs, *, bias=None, shift=0.0, masked_ids=(), canonical=
                    len(masked_ids), canonical.data_ptr() if canonical is not None else None,
                    out_dim, out.data_ptr(), _stream_ptr(stream)))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Encoder layer ops and the Qwen3 encoder runner (include/inl_encoder.h)
+# ---------------------------------------------------------------------------
+
+_linear_ws = _sig("inl_linear_workspace_size", ctypes.c_int, ctypes.POINTER(ctypes.c_size_t))
+_linear = _sig("inl_linear_fwd", ctypes.c_int, c_i64, c_i64, c_i64, c_i32, c_void_p, c_i64, c_void_p, c_i64,
+               c_i32, c_void_p, c_i64, ctypes.c_float, ctypes.c_float, c_void_p, ctypes.c_size_t, c_void_p)
+_embed = _sig("inl_embed_fwd", ctypes.c_int, c_i64, c_void_p, c_void_p, c_i64, c_i32, c_i32, c_void_p, c_i64,
+              c_void_p)
+_rms_rows = _sig("inl_rms_norm_rows_fwd", ctypes.c_int, c_i64, c_i32, c_void_p, c_i64, c_void_p, c_i32,
+                 ctypes.c_float, c_i32, c_void_p, c_i64, c_void_p)
+_swiglu = _sig("inl_swiglu_fwd", ctypes.c_int, c_i64, c_i32, c_i32, c_void_p, c_i64, c_void_p, c_i64, c_void_p)
+
+
+class Qwen3Config(ctypes.Structure):
+    _fields_ = [("vocab", c_i32), ("hidden", c_i32), ("intermediate", c_i32), ("layers", c_i32),
+                ("heads", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32), ("eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_double), ("max_positions", c_i32), ("dtype", c_i32),
+                ("attn_flags", c_i32)]
+
+
+class Qwen3LayerWeights(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("qkv_proj", "o_proj", "gate_up_proj", "down_proj", "q_norm", "k_norm",
+                                        "input_norm", "post_attention_norm")]
+
+
+_q3_create = _sig("inl_qwen3_create", ctypes.c_int, ctypes.POINTER(Qwen3Config), c_void_p,
+                  ctypes.POINTER(Qwen3LayerWeights), c_void_p, ctypes.POINTER(c_void_p))
+_q3_destroy = _sig("inl_qwen3_destroy", ctypes.c_int, c_void_p)
+_q3_ws = _sig("inl_qwen3_workspace_size", ctypes.c_int, c_void_p, c_i32, c_void_p, ctypes.POINTER(ctypes.c_size_t))
+_q3_encode = _sig("inl_qwen3_encode", ctypes.c_int, c_void_p, c_i32, c_void_p, c_void_p, c_void_p, c_void_p,
+                  ctypes.c_size_t, c_void_p)
+
+_LINEAR_WS = {}
+
+
+def _linear_workspace(dev):
+    import torch
+    key = str(dev)
+    if key not in _LINEAR_WS:
+        n = ctypes.c_size_t()
+        _check(_linear_ws(ctypes.byref(n)))
+        _LINEAR_WS[key] = torch.empty(n.value, dtype=torch.uint8, device=dev)
+    return _LINEAR_WS[key]
+
+
+def linear(x, w, *, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=None):
+    """``out = alpha * x @ w.T + beta * out`` on hipBLASLt (``inl_linear_fwd``):
+    ``x [m, k]``, ``w [n, k]`` row-major, rows may be strided."""
+    import torch
+    m, k = x.shape
+    n = w.shape[0]
+    if w.shape[1] != k or x.dtype != w.dtype:
+        raise InlError(-1, "linear: x [m, k] and w [n, k] must agree in k and dtype")
+    if x.stride(1) != 1 or w.stride(1) != 1:
+        raise InlError(-1, "linear: rows must be contiguous")
+    od = out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype)
+    if out is None:
+        out = torch.empty((m, n), dtype=od, device=x.device)
+    if out.shape != (m, n) or out.stride(1) != 1:
+        raise InlError(-1, f"linear: out must be [{m}, {n}] with contiguous rows")
+    ws = _linear_workspace(x.device)
+    _check(_linear(m, n, k, _dtype_code(x.dtype), x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                   _dtype_code(out.dtype), out.data_ptr(), out.stride(0), float(alpha), float(beta),
+                   ws.data_ptr(), ws.numel(), _stream_ptr(stream)))
+    return out
+
+
+def embed(ids, table, *, stream=None):
+    """``table[ids]`` as f32 rows (``inl_embed_fwd``); ids int32 on the device."""
+    import torch
+    out = torch.empty((ids.numel(), table.shape[1]), dtype=torch.float32, device=table.device)
+    _check(_embed(ids.numel(), ids.data_ptr(), table.data_ptr(), table.shape[0], table.shape[1],
+                  _dtype_code(table.dtype), out.data_ptr(), out.stride(0), _stream_ptr(stream)))
+    return out
+
+
+def rms_norm_rows(x, weight=None, *, eps=1e-6, out_dtype=None, stream=None):
+    """RMSNorm of f32 rows into ``out_dtype`` (``inl_rms_norm_rows_fwd``)."""
+    import torch
+    rows, dim = x.shape
+    od = out_dtype if out_dtype is not None else torch.float32
+    out = torch.empty((rows, dim), dtype=od, device=x.device)
+    wdt = _dtype_code(weight.dtype) if weight is not None else INL_F32
+    _check(_rms_rows(rows, dim, x.data_ptr(), x.stride(0), weight.data_ptr() if weight is not None else None,
+                     wdt, float(eps), _dtype_code(od), out.data_ptr(), out.stride(0), _stream_ptr(stream)))
+    return out
+
+
+def swiglu(gate_up, intermediate, *, stream=None):
+    """``silu(gate_up[:, :I]) * gate_up[:, I:2I]`` (``inl_swiglu_fwd``)."""
+    import torch
+    rows = gate_up.shape[0]
+    out = torch.empty((rows, intermediate), dtype=gate_up.dtype, device=gate_up.device)
+    _check(_swiglu(rows, intermediate, _dtype_code(gate_up.dtype), gate_up.data_ptr(), gate_up.stride(0),
+                   out.data_ptr(), out.stride(0), _stream_ptr(stream)))
+    return out
+
+
+class Qwen3Encoder:
+    """The GPU Qwen3 embedder (``inl_qwen3_*``): packed texts in, unit-length
+    last-token embeddings out. ``weights`` maps the checkpoint's tensor names
+    (``embed_tokens.weight``, ``layers.{i}.self_attn.q_proj.weight``, ...,
+    ``norm.weight``) to device tensors of one dtype; the q/k/v and gate/up
+    projections are stacked once here (the runner takes them fused)."""
+
+    def __init__(self, cfg, weights, *, max_positions=4096, attn_flags=0):
+        import torch
+        t0 = weights["embed_tokens.weight"]
+        self.dtype = t0.dtype
+        self.cfg = cfg
+        c = Qwen3Config()
+        c.vocab, c.hidden, c.intermediate, c.layers = cfg.vocab, cfg.hidden, cfg.intermediate, cfg.layers
+        c.heads, c.kv_heads, c.head_dim = cfg.heads, cfg.kv_heads, cfg.head_dim
+        c.eps, c.rope_theta, c.max_positions = cfg.eps, cfg.theta, max_positions
+        c.dtype, c.attn_flags = _dtype_code(self.dtype), attn_flags
+        self._keep = [t0, weights["norm.weight"]]
+        layers = (Qwen3LayerWeights * cfg.layers)()
+        for i in range(cfg.layers):
+            p = f"layers.{i}."
+            W = lambda n: weights[p + n].contiguous()
+            qkv = torch.cat([W("self_attn.q_proj.weight"), W("self_attn.k_proj.weight"),
+                             W("self_attn.v_proj.weight")], 0).contiguous()
+            gu = torch.cat([W("mlp.gate_proj.weight"), W("mlp.up_proj.weight")], 0).contiguous()
+            parts = [qkv, W("self_attn.o_proj.weight"), gu, W("mlp.down_proj.weight"), W("self_attn.q_norm.weight"),
+                     W("self_attn.k_norm.weight"), W("input_layernorm.weight"),
+                     W("post_attention_layernorm.weight")]
+            for t in parts:
+                if t.dtype != self.dtype or not t.is_cuda:
+                    raise InlError(-1, f"layer {i}: every weight must be a {self.dtype} device tensor")
+            self._keep += parts
+            for name, t in zip([f[0] for f in Qwen3LayerWeights._fields_], parts):
+                setattr(layers[i], name, t.data_ptr())
+        h = c_void_p()
+        _check(_q3_create(ctypes.byref(c), t0.data_ptr(), layers, weights["norm.weight"].data_ptr(), ctypes.byref(h)))
+        self._h = h
+
+    def workspace_bytes(self, cu_seqlens) -> int:
+        cu = _cu_array(cu_seqlens)
+        n = ctypes.c_size_t()
+        _check(_q3_ws(self._h, len(cu_seqlens) - 1, cu, ctypes.byref(n)))
+        return n.value
+
+    def encode(self, ids, cu_seqlens, *, out=None, workspace=None, stream=None):
+        """``ids``: host int sequence of the packed token ids; returns f32
+        ``[texts, hidden]`` unit vectors on the device."""
+        import numpy as np
+        import torch
+        cu = _cu_array(cu_seqlens)
+        nt = len(cu_seqlens) - 1
+        idv = np.ascontiguousarray(ids, dtype=np.int32)
+        if len(idv) != int(cu_seqlens[-1]):
+            raise InlError(-1, f"encode: {len(idv)} ids for {int(cu_seqlens[-1])} tokens")
+        dev = self._keep[0].device
+        if out is None:
+            out = torch.empty((nt, self.cfg.hidden), dtype=torch.float32, device=dev)
+        need = self.workspace_bytes(cu_seqlens)
+        if workspace is None or workspace.numel() < need:
+            workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+        ptr = workspace.data_ptr()
+        ptr += (-ptr) % 256
+        _check(_q3_encode(self._h, nt, cu, idv.ctypes.data, out.data_ptr(), ptr, need, _stream_ptr(stream)))
+        self._last_ws = workspace
+        return out
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _check(_q3_destroy(self._h))
+            self._h = c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

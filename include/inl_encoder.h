@@ -1,0 +1,136 @@
+/*
+ * inl_encoder.h - C ABI of the layer ops around the attention path and of a
+ * whole-encoder runner, on one MI355X (gfx950).
+ *
+ * The reference runs an encoder's projections, norms and MLP as candle ops
+ * (crates/inl-text/src/qwen3/mod.rs:72-116,227-297,339-358). The calls below
+ * are their GPU counterparts, so that an engine's forward runs on the device
+ * end to end: the GEMMs on hipBLASLt (inl_linear_fwd), the element-wise ops
+ * on the library's own kernels. Conventions are those of inl_hip.h (device
+ * pointers unless named `_host`, int status + inl_last_error(), work on the
+ * caller's stream, the caller owns every buffer).
+ */
+#ifndef INL_ENCODER_H
+#define INL_ENCODER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "inl_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------
+ * Layer ops
+ * --------------------------------------------------------------------- */
+
+/* y[m, n] = alpha * x[m, k] . w[n, k]^T + beta * y: a bias-free candle
+ * `Linear` (qwen3/mod.rs:99-104, q/k/v/o projections :188-209, gate/up/down
+ * :96-106) with its row-major [out, in] weight. beta = 1 accumulates into y,
+ * which is how a residual addition (qwen3/mod.rs:291-296) folds into the
+ * o_proj and down_proj GEMMs. dtypes: f32 -> f32, bf16 -> bf16, bf16 -> f32.
+ * Strides are elements between rows (0 = packed). `workspace` (device, may be
+ * NULL with 0 bytes) lets hipBLASLt pick kernels that need scratch; size it
+ * with inl_linear_workspace_size. Runs hipBLASLt; per device and shape the
+ * first call queries its heuristic, later calls reuse the choice. */
+int inl_linear_workspace_size(size_t* bytes);
+int inl_linear_fwd(int64_t m, int64_t n, int64_t k, int32_t in_dtype,
+                   const void* x, int64_t x_stride, const void* w,
+                   int64_t w_stride, int32_t out_dtype, void* y,
+                   int64_t y_stride, float alpha, float beta, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* out[t, :] = f32(table[ids[t], :]): the token embedding (candle Embedding,
+ * qwen3/mod.rs:322-323,350) into an f32 residual stream. ids are device
+ * int32; an id outside [0, vocab) yields a NaN row (check ids first). */
+int inl_embed_fwd(int64_t n_tokens, const int32_t* ids, const void* table,
+                  int64_t vocab, int32_t hidden, int32_t dtype, float* out,
+                  int64_t out_stride, void* stream);
+
+/* y = x / sqrt(mean(x^2) + eps) * weight per row of an f32 stream x, written
+ * in out_dtype: the pre-norm RMSNorm of qwen3/mod.rs:72-90 (input_layernorm,
+ * post_attention_layernorm :287-295). weight NULL = ones. dim and x_stride
+ * multiples of 4, x 16-byte aligned. */
+int inl_rms_norm_rows_fwd(int64_t rows, int32_t dim, const float* x,
+                          int64_t x_stride, const void* weight,
+                          int32_t weight_dtype, float eps, int32_t out_dtype,
+                          void* y, int64_t y_stride, void* stream);
+
+/* out[t, i] = silu(gate_up[t, i]) * gate_up[t, intermediate + i], silu(g) =
+ * g / (1 + exp(-g)) in f32: the MLP gate of qwen3/mod.rs:109-116 over a fused
+ * gate/up projection output (gate rows first). Sizes and strides 16-byte
+ * multiples. */
+int inl_swiglu_fwd(int64_t rows, int32_t intermediate, int32_t dtype,
+                   const void* gate_up, int64_t gu_stride, void* out,
+                   int64_t out_stride, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Qwen3 encoder runner: the GPU counterpart of Qwen3Model::forward_last and
+ * Qwen3Embedder::embed (crates/inl-text/src/qwen3/mod.rs:339-358,438-470)
+ * over packed texts (each text's last row pooled; positions restart at 0 per
+ * text, as in the reference's left-padded batch). The weights stay the
+ * caller's; two projections are fused by stacking rows:
+ *   qkv_proj:     [(heads + 2 kv_heads) * head_dim, hidden] = q_proj rows,
+ *                 then k_proj rows, then v_proj rows;
+ *   gate_up_proj: [2 * intermediate, hidden] = gate_proj rows, then up_proj.
+ * All weights are in `dtype` (INL_F32 or INL_BF16). The residual stream is
+ * f32 in both modes; GEMM inputs and attention run in `dtype`.
+ * --------------------------------------------------------------------- */
+typedef struct inl_qwen3_config {
+  int32_t vocab;
+  int32_t hidden;
+  int32_t intermediate;
+  int32_t layers;
+  int32_t heads;
+  int32_t kv_heads;
+  int32_t head_dim;       /* 128 for the benchmark shape */
+  float eps;              /* rms_norm_eps */
+  double rope_theta;
+  int32_t max_positions;  /* longest text the RoPE table covers */
+  int32_t dtype;          /* enum inl_dtype of the weights and activations */
+  int32_t attn_flags;     /* INL_ATTN_* (INL_ATTN_PV_BF16 for V beyond fp16) */
+} inl_qwen3_config;
+
+typedef struct inl_qwen3_layer_weights {
+  const void* qkv_proj;
+  const void* o_proj;         /* [hidden, heads * head_dim] */
+  const void* gate_up_proj;
+  const void* down_proj;      /* [hidden, intermediate] */
+  const void* q_norm;         /* [head_dim] */
+  const void* k_norm;         /* [head_dim] */
+  const void* input_norm;     /* [hidden] */
+  const void* post_attention_norm; /* [hidden] */
+} inl_qwen3_layer_weights;
+
+typedef struct inl_qwen3 inl_qwen3;
+
+/* Keeps the weight pointers (and copies the layer table); builds the RoPE
+ * tables (f64 angles, qwen3/mod.rs:131-153) and an f32 copy of the final
+ * norm on the current device - the only allocations the runner makes. */
+int inl_qwen3_create(const inl_qwen3_config* cfg, const void* embed_tokens,
+                     const inl_qwen3_layer_weights* layers,
+                     const void* final_norm, inl_qwen3** enc);
+int inl_qwen3_destroy(inl_qwen3* enc);
+
+/* Device workspace one encode of these texts needs (activations, the
+ * attention schedule, the GEMM workspace). */
+int inl_qwen3_workspace_size(const inl_qwen3* enc, int32_t n_texts,
+                             const int32_t* cu_seqlens_host, size_t* bytes);
+
+/* embeddings[b, :] (device f32 [n_texts, hidden]) = L2-normalised final
+ * RMSNorm of text b's last row (+1e-12 inside the square root,
+ * qwen3/mod.rs:468). ids_host: [cu_seqlens_host[n_texts]] token ids, checked
+ * against vocab on the host. Texts of length 0 are refused, as the
+ * reference refuses an empty tokenisation (qwen3/mod.rs:446-448). */
+int inl_qwen3_encode(inl_qwen3* enc, int32_t n_texts,
+                     const int32_t* cu_seqlens_host, const int32_t* ids_host,
+                     float* embeddings, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INL_ENCODER_H */

@@ -113,6 +113,14 @@ typedef struct inl_attn_plan inl_attn_plan;
  * current when it is created: its schedule lives there, and the kernel's
  * launch attributes are set there once, so inl_attn_fwd takes no lock. */
 int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** plan);
+/* The same plan with its schedule in the caller's device `workspace` (at
+ * least inl_attn_workspace_size() bytes, 16-byte aligned), uploaded
+ * asynchronously on `stream` from pageable host memory: nothing is allocated
+ * on the device. The workspace must outlive the plan's launches; destroying
+ * the plan does not free it. */
+int inl_attn_plan_create_in(const inl_attn_desc* desc, void* workspace,
+                            size_t workspace_bytes, void* stream,
+                            inl_attn_plan** plan);
 int inl_attn_plan_destroy(inl_attn_plan* plan);
 /* Tiles the plan launches and query rows each covers (for reporting). */
 int inl_attn_plan_info(const inl_attn_plan* plan, int64_t* n_tiles,

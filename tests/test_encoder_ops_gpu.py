@@ -1,0 +1,99 @@
+"""GPU parity of the encoder's layer ops (include/inl_encoder.h) through the
+C ABI: the hipBLASLt Linear against a plain PyTorch fp32 reference of the same
+product (and the oracle's formula for the element-wise ops).
+
+Tolerances: f32 GEMMs within 1e-5 relative to the output's scale (f32 MFMA
+products, f32 accumulation in a different order); bf16 GEMMs within 2^-8
+relative of the f32 reference plus the output rounding (bf16 inputs are exact
+in f32, so only the accumulation order and the final rounding differ);
+element-wise ops within 1e-6 (f32) or half a bf16 ulp (bf16 output).
+"""
+import numpy as np
+import pytest
+
+from oracle import prologue as op
+from oracle import qwen3 as oq
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(torch, dev, shape, seed, scale=1.0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(*shape, generator=g, device=dev) * scale
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 32), (778, 4096, 1024), (777, 1024, 3072), (33, 6144, 1024)])
+def test_linear_f32(m, n, k, cuda, inl):
+    import torch
+    x = _rand(torch, cuda, (m, k), 1)
+    w = _rand(torch, cuda, (n, k), 2, k ** -0.5)
+    print(f"case=linear_f32 m={m} n={n} k={k}", flush=True)
+    y = inl.linear(x, w)
+    ref = x.double() @ w.double().T
+    torch.cuda.synchronize()
+    err = (y.double() - ref).abs().max().item() / ref.abs().max().item()
+    assert err <= 1e-5, err
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32_accumulate"])
+def test_linear_bf16(out, cuda, inl):
+    """bf16 inputs into bf16 output, and into an f32 output with beta = 1 (the
+    residual-add form of the o_proj and down_proj GEMMs); strided x rows."""
+    import torch
+    m, n, k = 300, 1024, 2048
+    xs = _rand(torch, cuda, (m, k + 64), 3).to(torch.bfloat16)
+    x = xs[:, :k]
+    w = _rand(torch, cuda, (n, k), 4, k ** -0.5).to(torch.bfloat16)
+    ref = x.double() @ w.double().T
+    print(f"case=linear_bf16 out={out}", flush=True)
+    if out == "bf16":
+        y = inl.linear(x, w)
+        torch.cuda.synchronize()
+        assert y.dtype == torch.bfloat16
+        bound = 2.0 ** -8 * ref.abs() + 2.0 ** -8 * ref.abs().max() * 1e-2
+        assert ((y.double() - ref).abs() <= bound + 1e-6).all()
+    else:
+        base = _rand(torch, cuda, (m, n), 5)
+        y = base.clone()
+        inl.linear(x, w, out=y, beta=1.0)
+        torch.cuda.synchronize()
+        err = (y.double() - (base.double() + ref)).abs().max().item()
+        assert err <= 1e-4 * ref.abs().max().item(), err
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_embed_rms_swiglu(dtype, cuda, inl):
+    import torch
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    vocab, hidden, inter, n = 500, 1024, 3072, 257
+    table = _rand(torch, cuda, (vocab, hidden), 6).to(td)
+    ids = torch.from_numpy(np.random.default_rng(0).integers(0, vocab, n).astype(np.int32)).to(cuda)
+    print(f"case=embed_rms_swiglu {dtype}", flush=True)
+    e = inl.embed(ids, table)
+    torch.cuda.synchronize()
+    assert e.dtype == torch.float32 and torch.equal(e, table.float()[ids.long()])
+    # an id outside the vocabulary gives a NaN row, not an out-of-range read
+    bad = inl.embed(torch.tensor([vocab, -1, 3], dtype=torch.int32, device=cuda), table)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad[:2]).all() and torch.equal(bad[2], table.float()[3])
+
+    w = (1 + 0.2 * (_rand(torch, cuda, (hidden,), 7))).to(td)
+    y = inl.rms_norm_rows(e, w, eps=1e-6, out_dtype=td)
+    torch.cuda.synchronize()
+    ref = op.rms_norm(e.cpu().numpy().astype(np.float64), w.float().cpu().numpy().astype(np.float64), 1e-6)
+    got = y.float().cpu().numpy()
+    if dtype == "f32":
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+    else:
+        assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6)
+
+    gu = _rand(torch, cuda, (n, 2 * inter), 8, 2.0).to(td)
+    a = inl.swiglu(gu, inter)
+    torch.cuda.synchronize()
+    g64 = gu.float().cpu().numpy().astype(np.float64)
+    ref = oq.silu(g64[:, :inter]) * g64[:, inter:]
+    got = a.float().cpu().numpy()
+    if dtype == "f32":
+        assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    else:
+        assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-5)
