@@ -185,7 +185,7 @@ def roofline(tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch):
                       "frac": round(gbs / PEAK_HBM_GBS, 4)}}
 
 
-OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade")
+OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade", "splade_decoder")
 E2E_WORKLOADS = ("qwen3_e2e", "qwen3_e2e_bf16")
 PEAK_F32_TFLOPS = 157.3     # dense fp32 matrix peak
 
@@ -379,6 +379,23 @@ def op_workload(name, torch, inl_hip, dev):
         label = (f"config4 SPLADE epilogue: max over {S} speaking rows x {V} f32 logits of 128 texts "
                  f"U[32,2048], finish (shift 10), fold to {terms} terms")
         return label, "splade_kernel", 1, timed(launches), S, nbytes, "f32"
+    if name == "splade_decoder":
+        # config 4: the fused decoder GEMM + per-text max over every speaking
+        # row (bf16 head [S, 768] x decoder [50002, 768]^T), no logits written
+        import numpy as np
+        lens = w.uniform_lengths(128, 32, 2048)
+        speak = [t - 1 for t in lens]
+        offs = np.asarray(w.cu_seqlens(speak), dtype=np.int32)
+        S, V, H = int(offs[-1]), 50002, 768
+        head = torch.randn(S, H, generator=g, device=dev).to(torch.bfloat16)
+        wd = (torch.randn(V, H, generator=g, device=dev) * (4.0 / H ** 0.5)).to(torch.bfloat16)
+        out = torch.empty(len(speak), V, device=dev)
+        launches = [lambda: inl_hip.splade_decoder_max(head, wd, offs, out=out, stream=stream)]
+        flops = 2 * S * V * H
+        label = (f"config4 SPLADE decoder GEMM + per-text max, fused: {S} speaking rows x {V} terms x {H} "
+                 f"(bf16, f32 accumulation) of 128 texts U[32,2048]; the {S * V * 4 / 1e9:.1f} GB of f32 logits "
+                 "are never written")
+        return label, "splade_decoder_max_kernel", 1, timed(launches), S, flops, "bf16"
     raise SystemExit(f"unknown op workload {name}")
 
 
@@ -408,7 +425,8 @@ def op_main(args):
     import inl_hip
     dev = torch.device("cuda:0")
     label, kernel, n_launch, step, tokens, nbytes, dtype = op_workload(args.workload, torch, inl_hip, dev)
-    log(f"workload: {label}; {nbytes / 1e9:.3f} GB per step, {n_launch} launches")
+    mfma = args.workload == "splade_decoder"   # a GEMM: its work is flops, not bytes
+    log(f"workload: {label}; {nbytes / 1e9:.3f} {'GFLOP' if mfma else 'GB'} per step, {n_launch} launches")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -419,18 +437,24 @@ def op_main(args):
     wall = time.perf_counter() - t0
     avg_ms = timed_launches(torch, step, n_launch, args.steps)
     gbs = nbytes / n_launch / (avg_ms * 1e-3) / 1e9
+    if mfma:
+        tf = nbytes / n_launch / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic(args.workload), "kernel": kernel,
+                "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"flop": nbytes / n_launch}}
+    else:
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": read_traffic(args.workload), "kernel": kernel,
+                "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"hbm_bytes": nbytes / n_launch}}
     print(json.dumps({
-        "metric": f"{args.workload} op throughput (HBM GB/s vs 8 TB/s)",
+        "metric": f"{args.workload} op throughput ({'TFLOP/s vs bf16 MFMA peak' if mfma else 'HBM GB/s vs 8 TB/s'})",
         "value": round(tokens * args.steps / wall, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (seeded random inputs; no checkpoint)",
         "config": {"workload": label, "tokens_per_step": tokens, "launches_per_step": n_launch,
-                   "hbm_bytes_per_step": nbytes},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": read_traffic(args.workload), "kernel": kernel,
-                     "avg_launch_us": round(avg_ms * 1e3, 2),
-                     "algorithmic_per_launch": {"hbm_bytes": nbytes / n_launch}},
+                   ("flop_per_step" if mfma else "hbm_bytes_per_step"): nbytes},
+        "roofline": roof,
     }), flush=True)
 
 

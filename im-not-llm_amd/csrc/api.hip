@@ -1,7 +1,10 @@
 // Error reporting and argument checks shared by the library's entry points.
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "inl_common.hpp"
 
@@ -31,6 +34,18 @@ int check_cu(int32_t n, const int32_t* cu, int64_t* total) {
   for (int32_t b = 0; b < n; ++b)
     if (cu[b + 1] < cu[b]) return fail(INL_E_INVALID, "cu_seqlens must be nondecreasing");
   *total = cu[n];
+  return INL_OK;
+}
+
+int set_max_dynamic_lds(const void* fn, int bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  INL_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({fn, dev})) return INL_OK;
+  INL_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+  done.insert({fn, dev});
   return INL_OK;
 }
 

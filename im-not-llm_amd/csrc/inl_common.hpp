@@ -37,6 +37,9 @@ int hip_fail(hipError_t err, const char* what);
 inline int dtype_size(int32_t dt) { return dt == INL_BF16 ? 2 : 4; }
 inline bool dtype_ok(int32_t dt) { return dt == INL_F32 || dt == INL_BF16; }
 
+// Raise a kernel's dynamic LDS limit to `bytes`, once per (kernel, device).
+int set_max_dynamic_lds(const void* fn, int bytes);
+
 // Validate cu_seqlens (host): cu[0] == 0 and nondecreasing. Returns the token
 // count through `total`.
 int check_cu(int32_t n, const int32_t* cu, int64_t* total);

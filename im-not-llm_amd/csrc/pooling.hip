@@ -176,6 +176,7 @@ struct SpladeParams {
   const float* bias;       // [vocab] or null
   const int32_t* canonical;  // [vocab] or null
   float* out;
+  int32_t direct;          // 1: logits already hold each row's maximum (offs unused)
   int32_t vocab, out_dim, n_masked;
   float shift;
   int32_t masked[kMaxMasked];
@@ -190,7 +191,7 @@ __global__ __launch_bounds__(256) void splade_kernel(SpladeParams p) {
   const int r = blockIdx.y;
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= p.vocab) return;
-  const int32_t a = p.offs[r], e = p.offs[r + 1];
+  const int32_t a = p.direct ? r : p.offs[r], e = p.direct ? r + 1 : p.offs[r + 1];
   // running max over the row's speaking positions (4 independent chains)
   float m0 = -INFINITY, m1 = -INFINITY, m2 = -INFINITY, m3 = -INFINITY;
   const float* col = p.logits + t;
@@ -299,17 +300,45 @@ extern "C" int inl_l2_normalize_fwd(int32_t rows, int32_t dim, int64_t in_stride
   return INL_OK;
 }
 
+namespace inl {
+namespace {
+
+int splade_launch(int32_t rows, const int32_t* offs, int32_t vocab, const float* logits, int64_t logits_stride,
+                  const float* bias, float shift, const int32_t* masked_ids_host, int32_t n_masked,
+                  const int32_t* canonical, int32_t out_dim, float* out, void* stream, bool direct);
+
+}  // namespace
+}  // namespace inl
+
 extern "C" int inl_pool_splade_fwd(int32_t rows, const int32_t* offs, int32_t vocab, const float* logits,
                                    int64_t logits_stride, const float* bias, float shift,
                                    const int32_t* masked_ids_host, int32_t n_masked, const int32_t* canonical,
                                    int32_t out_dim, float* out, void* stream) {
-  using namespace inl;
+  if (rows > 0 && !offs) return inl::fail(INL_E_INVALID, "pool_splade: NULL pointer or bad stride");
+  return inl::splade_launch(rows, offs, vocab, logits, logits_stride, bias, shift, masked_ids_host, n_masked,
+                            canonical, out_dim, out, stream, false);
+}
+
+extern "C" int inl_splade_finish_fwd(int32_t rows, int32_t vocab, const float* maxima, int64_t maxima_stride,
+                                     const float* bias, float shift, const int32_t* masked_ids_host,
+                                     int32_t n_masked, const int32_t* canonical, int32_t out_dim, float* out,
+                                     void* stream) {
+  return inl::splade_launch(rows, nullptr, vocab, maxima, maxima_stride, bias, shift, masked_ids_host, n_masked,
+                            canonical, out_dim, out, stream, true);
+}
+
+namespace inl {
+namespace {
+
+int splade_launch(int32_t rows, const int32_t* offs, int32_t vocab, const float* logits, int64_t logits_stride,
+                  const float* bias, float shift, const int32_t* masked_ids_host, int32_t n_masked,
+                  const int32_t* canonical, int32_t out_dim, float* out, void* stream, bool direct) {
   if (rows < 0 || vocab <= 0 || n_masked < 0 || out_dim <= 0) return fail(INL_E_INVALID, "pool_splade: bad arguments");
   if (n_masked > kMaxMasked) return fail(INL_E_UNSUPPORTED, "pool_splade: more than 16 masked vocabulary ids");
   if (!canonical && out_dim != vocab) return fail(INL_E_INVALID, "pool_splade: out_dim must equal vocab without canonical ids");
   if (rows == 0) return INL_OK;
   const int64_t ls = logits_stride ? logits_stride : vocab;
-  if (!offs || !logits || !out || ls < vocab || (n_masked && !masked_ids_host))
+  if (!logits || !out || ls < vocab || (n_masked && !masked_ids_host))
     return fail(INL_E_INVALID, "pool_splade: NULL pointer or bad stride");
   if (rows > 65535) return fail(INL_E_UNSUPPORTED, "pool_splade: more than 65535 rows in one call");
   SpladeParams p{};
@@ -323,6 +352,7 @@ extern "C" int inl_pool_splade_fwd(int32_t rows, const int32_t* offs, int32_t vo
   p.out_dim = out_dim;
   p.shift = shift;
   p.n_masked = n_masked;
+  p.direct = direct;
   for (int k = 0; k < n_masked; ++k) {
     if (masked_ids_host[k] < 0 || masked_ids_host[k] >= vocab)
       return fail(INL_E_INVALID, "pool_splade: masked id outside the vocabulary");
@@ -338,3 +368,6 @@ extern "C" int inl_pool_splade_fwd(int32_t rows, const int32_t* offs, int32_t vo
   INL_HIP_TRY(hipGetLastError());
   return INL_OK;
 }
+
+}  // namespace
+}  // namespace inl

@@ -663,3 +663,53 @@ class Qwen3Encoder:
             self.close()
         except Exception:
             pass
+
+
+_sd_ws = _sig("inl_splade_decoder_workspace_size", ctypes.c_int, c_i32, c_i32, ctypes.POINTER(ctypes.c_size_t))
+_sd_max = _sig("inl_splade_decoder_max_fwd", ctypes.c_int, c_i32, c_void_p, c_void_p, c_i64, c_i32, c_void_p, c_i64,
+               c_i32, c_i32, c_void_p, c_void_p, ctypes.c_size_t, c_void_p)
+_sp_finish = _sig("inl_splade_finish_fwd", ctypes.c_int, c_i32, c_i32, c_void_p, c_i64, c_void_p, ctypes.c_float,
+                  c_void_p, c_i32, c_void_p, c_i32, c_void_p, c_void_p)
+
+
+def splade_decoder_max(head, w_dec, offs, *, out=None, stream=None):
+    """Per-text maxima over speaking positions of ``head @ w_dec.T`` without
+    materialising the logits (``inl_splade_decoder_max_fwd``): ``head [S, H]``
+    and ``w_dec [V, H]`` bf16 device tensors, ``offs`` a host sequence of
+    ``rows + 1`` position offsets. Returns f32 ``[rows, V]``."""
+    import numpy as np
+    import torch
+    rows = len(offs) - 1
+    S, H = head.shape
+    V = w_dec.shape[0]
+    if w_dec.shape[1] != H or head.dtype != w_dec.dtype:
+        raise InlError(-1, "splade_decoder_max: head [S, H] and w_dec [V, H] must agree in H and dtype")
+    if int(offs[-1]) > S:
+        raise InlError(-1, f"splade_decoder_max: offsets cover {int(offs[-1])} positions, head has {S}")
+    if head.stride(1) != 1 or w_dec.stride(1) != 1:
+        raise InlError(-1, "splade_decoder_max: rows must be contiguous")
+    if out is None:
+        out = torch.empty((rows, V), dtype=torch.float32, device=head.device)
+    ofs = np.ascontiguousarray(offs, dtype=np.int32)
+    n = ctypes.c_size_t()
+    _check(_sd_ws(rows, V, ctypes.byref(n)))
+    ws = torch.empty(n.value, dtype=torch.uint8, device=head.device)
+    _check(_sd_max(rows, ofs.ctypes.data, head.data_ptr(), head.stride(0), H, w_dec.data_ptr(), w_dec.stride(0),
+                   V, _dtype_code(head.dtype), out.data_ptr(), ws.data_ptr(), n.value, _stream_ptr(stream)))
+    out._inl_workspace = ws
+    return out
+
+
+def splade_finish(maxima, *, bias=None, shift=0.0, masked_ids=(), canonical=None, out_dim=None, stream=None):
+    """``inl_splade_finish_fwd``: finish and fold per-row maxima [rows, V]."""
+    import torch
+    rows, vocab = maxima.shape
+    if out_dim is None:
+        out_dim = vocab if canonical is None else int(canonical.max().item()) + 1
+    out = torch.empty((rows, out_dim), dtype=torch.float32, device=maxima.device)
+    m = (c_i32 * max(1, len(masked_ids)))(*[int(v) for v in masked_ids])
+    _check(_sp_finish(rows, vocab, maxima.data_ptr(), maxima.stride(0),
+                      bias.data_ptr() if bias is not None else None, float(shift), m, len(masked_ids),
+                      canonical.data_ptr() if canonical is not None else None, out_dim, out.data_ptr(),
+                      _stream_ptr(stream)))
+    return out

@@ -67,6 +67,28 @@ int inl_swiglu_fwd(int64_t rows, int32_t intermediate, int32_t dtype,
                    int64_t out_stride, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Fused SPLADE decoder + max (crates/inl-sparse/src/modernbert.rs:657-662
+ * `project`'s bias-free decoder, :806-872 `pool_states`'s per-row max):
+ *   out[r, v] = max over p in [offs_host[r], offs_host[r+1]) of
+ *               head[p, :] . w_dec[v, :]        (f32; -inf without positions)
+ * for the packed MLM-head outputs of every speaking position (head
+ * [S, hidden], bf16) and the decoder weight w_dec [vocab, hidden] (bf16),
+ * without writing the [S, vocab] logits. Feed `out` to inl_splade_finish_fwd
+ * (inl_hip.h) for the bias, shift, relu, log1p, mask and canonical fold.
+ * hidden a multiple of 32; strides in elements, 16-byte multiples. The
+ * workspace (device, 16-byte aligned) holds the launch schedule. The max is
+ * taken over f32 products accumulated in f32 on the matrix cores: for given
+ * bf16 inputs it differs from a sequential f32 sum only in rounding.
+ * --------------------------------------------------------------------- */
+int inl_splade_decoder_workspace_size(int32_t rows, int32_t vocab, size_t* bytes);
+int inl_splade_decoder_max_fwd(int32_t rows, const int32_t* offs_host,
+                               const void* head, int64_t head_stride,
+                               int32_t hidden, const void* w_dec,
+                               int64_t w_stride, int32_t vocab, int32_t dtype,
+                               float* out, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Qwen3 encoder runner: the GPU counterpart of Qwen3Model::forward_last and
  * Qwen3Embedder::embed (crates/inl-text/src/qwen3/mod.rs:339-358,438-470)
  * over packed texts (each text's last row pooled; positions restart at 0 per

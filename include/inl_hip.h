@@ -278,6 +278,17 @@ int inl_pool_splade_fwd(int32_t rows, const int32_t* offs, int32_t vocab,
                         const int32_t* canonical, int32_t out_dim, float* out,
                         void* stream);
 
+/* The finish and fold of inl_pool_splade_fwd applied to per-row maxima that
+ * are already known (`maxima` [rows, vocab] f32, -inf for a silent row, e.g.
+ * from inl_splade_decoder_max_fwd): out[r, c] = max(0, max over t with
+ * canonical[t] == c of ln(relu(maxima[r, t] + bias[t] - shift) * open[t] + 1))
+ * (crates/inl-sparse/src/modernbert.rs:874-907). */
+int inl_splade_finish_fwd(int32_t rows, int32_t vocab, const float* maxima,
+                          int64_t maxima_stride, const float* bias, float shift,
+                          const int32_t* masked_ids_host, int32_t n_masked,
+                          const int32_t* canonical, int32_t out_dim, float* out,
+                          void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Packed batch planner (host). Replaces the padded planners of the text,
  * sparse, late and vision engines (crates/inl-text/src/native.rs:698-735,
