@@ -713,3 +713,113 @@ def splade_finish(maxima, *, bias=None, shift=0.0, masked_ids=(), canonical=None
                       canonical.data_ptr() if canonical is not None else None, out_dim, out.data_ptr(),
                       _stream_ptr(stream)))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Gated-delta-net ops (include/inl_gdn.h)
+# ---------------------------------------------------------------------------
+
+_gdn_conv = _sig("inl_gdn_conv_fwd", ctypes.c_int, c_i64, c_i32, c_void_p, c_i32, c_i32, c_i32, c_void_p, c_i64,
+                 c_void_p, c_void_p, c_i64, c_void_p)
+_gdn_gates = _sig("inl_gdn_gates_fwd", ctypes.c_int, c_i64, c_i32, c_i32, c_void_p, c_i64, c_void_p, c_i64,
+                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p)
+_gdn_rule = _sig("inl_gdn_rule_fwd", ctypes.c_int, c_i64, c_i32, c_void_p, c_i32, c_i32, c_i32, c_i32, c_i32,
+                 c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p)
+_gdn_norm = _sig("inl_gdn_gated_norm_fwd", ctypes.c_int, c_i64, c_i32, c_i32, c_i32, c_i32, c_void_p, c_i64,
+                 c_void_p, c_i64, c_void_p, ctypes.c_float, c_void_p, c_i64, c_void_p)
+_gdn_inverse = _sig("inl_gdn_unit_lower_inverse_fwd", ctypes.c_int, c_i64, c_i32, c_void_p, c_void_p, c_void_p)
+
+
+def _cu_device(cu, device):
+    import torch
+    if isinstance(cu, torch.Tensor):
+        if cu.dtype != torch.int32 or not cu.is_cuda or cu.dim() != 1 or not cu.is_contiguous():
+            raise InlError(-1, "cu_seqlens must be a contiguous int32 device vector")
+        return cu
+    return torch.tensor([int(c) for c in cu], dtype=torch.int32, device=device)
+
+
+def _rows2d(x, name):
+    if x.dim() != 2 or x.stride(1) != 1 or not x.is_cuda:
+        raise InlError(-1, f"{name} must be a 2-D device tensor with unit column stride")
+
+
+def gdn_conv(x, cu_seqlens, weight, *, stream=None):
+    """``inl_gdn_conv_fwd``: silu(causal depthwise conv) per packed text; x
+    [N, C], weight [C, taps] (same dtype) -> [N, C]."""
+    import torch
+    _rows2d(x, "x")
+    cu = _cu_device(cu_seqlens, x.device)
+    n, ch = x.shape
+    weight = weight.contiguous()
+    if weight.dtype != x.dtype or weight.dim() != 2 or weight.shape[0] != ch:
+        raise InlError(-1, "weight must be [channels, taps] in x's dtype")
+    out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    _check(_gdn_conv(n, cu.numel() - 1, cu.data_ptr(), ch, weight.shape[1], _dtype_code(x.dtype), x.data_ptr(),
+                     x.stride(0), weight.data_ptr(), out.data_ptr(), out.stride(0), _stream_ptr(stream)))
+    return out
+
+
+def gdn_gates(a, b, dt_bias, neg_a, *, stream=None):
+    """``inl_gdn_gates_fwd``: (g, beta), f32 [N, nv], from the a/b projections."""
+    import torch
+    _rows2d(a, "a")
+    _rows2d(b, "b")
+    n, nv = a.shape
+    if b.shape != a.shape or b.dtype != a.dtype:
+        raise InlError(-1, "a and b must share shape and dtype")
+    dt_bias = dt_bias.float().contiguous()
+    neg_a = neg_a.float().contiguous()
+    g = torch.empty((n, nv), dtype=torch.float32, device=a.device)
+    beta = torch.empty_like(g)
+    _check(_gdn_gates(n, nv, _dtype_code(a.dtype), a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+                      dt_bias.data_ptr(), neg_a.data_ptr(), g.data_ptr(), beta.data_ptr(), _stream_ptr(stream)))
+    return g, beta
+
+
+def gdn_rule(mixed, cu_seqlens, key_heads, value_heads, key_dim, value_dim, g, beta, *, stream=None):
+    """``inl_gdn_rule_fwd``: the gated delta rule over packed texts; mixed
+    [N, 2 nk dk + nv dv] (model dtype), g/beta f32 [N, nv] -> f32 [N, nv, dv]."""
+    import torch
+    _rows2d(mixed, "mixed")
+    _rows2d(g, "g")
+    if beta.stride() != g.stride() or beta.shape != g.shape or g.dtype != torch.float32 or beta.dtype != torch.float32:
+        raise InlError(-1, "g and beta must be f32 tensors of one shape and stride")
+    cu = _cu_device(cu_seqlens, mixed.device)
+    n = mixed.shape[0]
+    if mixed.shape[1] != 2 * key_heads * key_dim + value_heads * value_dim or g.shape != (n, value_heads):
+        raise InlError(-1, "mixed must be [N, 2 nk dk + nv dv] and g [N, nv]")
+    out = torch.empty((n, value_heads, value_dim), dtype=torch.float32, device=mixed.device)
+    _check(_gdn_rule(n, cu.numel() - 1, cu.data_ptr(), key_heads, value_heads, key_dim, value_dim,
+                     _dtype_code(mixed.dtype), mixed.data_ptr(), mixed.stride(0), g.data_ptr(), beta.data_ptr(),
+                     g.stride(0), out.data_ptr(), out.stride(0), _stream_ptr(stream)))
+    return out
+
+
+def gdn_gated_norm(core, z, weight, eps, *, stream=None):
+    """``inl_gdn_gated_norm_fwd``: core [N, heads, dv] (f32 or z's dtype), z
+    [N, heads, dv], weight [dv] (z's dtype) -> [N, heads, dv] in z's dtype."""
+    import torch
+    if core.dim() != 3 or z.shape != core.shape or not core.is_contiguous() or not z.is_contiguous():
+        raise InlError(-1, "core and z must be contiguous [N, heads, dv] tensors")
+    n, heads, dv = core.shape
+    weight = weight.contiguous()
+    if weight.dtype != z.dtype or weight.numel() != dv:
+        raise InlError(-1, "weight must be [dv] in z's dtype")
+    out = torch.empty_like(z)
+    _check(_gdn_norm(n, heads, dv, _dtype_code(z.dtype), _dtype_code(core.dtype), core.data_ptr(), core.stride(0),
+                     z.data_ptr(), z.stride(0), weight.data_ptr(), float(eps), out.data_ptr(), out.stride(0),
+                     _stream_ptr(stream)))
+    return out
+
+
+def unit_lower_inverse(a, *, stream=None):
+    """``inl_gdn_unit_lower_inverse_fwd``: (I + A)^-1 of f32 [n, S, S]
+    strictly lower-triangular matrices."""
+    import torch
+    if a.dim() != 3 or a.shape[1] != a.shape[2] or a.dtype != torch.float32 or not a.is_cuda:
+        raise InlError(-1, "a must be an f32 device tensor [n, S, S]")
+    a = a.contiguous()
+    out = torch.empty_like(a)
+    _check(_gdn_inverse(a.shape[0], a.shape[1], a.data_ptr(), out.data_ptr(), _stream_ptr(stream)))
+    return out

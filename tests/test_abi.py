@@ -141,3 +141,39 @@ def test_binding_refuses_tensors_the_kernels_would_overrun():
     assert inl_hip.desc_rows(padded) == 16
     with pytest.raises(inl_hip.InlError, match="the desc covers 16"):
         inl_hip._check_tensors(padded, *good)
+
+
+def test_gdn_entry_points_validate_on_the_host():
+    """Shapes outside what the gated-delta-net kernels hold are refused
+    before any device call (null device pointers are never dereferenced)."""
+    import inl_hip
+    L = inl_hip._lib
+    bad = inl_hip.INL_E_INVALID if hasattr(inl_hip, "INL_E_INVALID") else -1
+    # taps beyond 8, zero channels
+    assert L.inl_gdn_conv_fwd(ctypes.c_int64(4), 1, None, 8, 9, 0, None, ctypes.c_int64(0), None, None,
+                              ctypes.c_int64(0), None) == bad
+    assert L.inl_gdn_conv_fwd(ctypes.c_int64(4), 1, None, 0, 4, 0, None, ctypes.c_int64(0), None, None,
+                              ctypes.c_int64(0), None) == bad
+    # no rows: nothing to do
+    assert L.inl_gdn_conv_fwd(ctypes.c_int64(0), 1, None, 8, 4, 0, None, ctypes.c_int64(0), None, None,
+                              ctypes.c_int64(0), None) == 0
+    # key_dim 129, value heads not a multiple of key heads
+    args = (ctypes.c_int64(4), 1, None)
+    assert L.inl_gdn_rule_fwd(*args, 1, 1, 129, 64, 0, None, ctypes.c_int64(0), None, None, ctypes.c_int64(0),
+                              None, ctypes.c_int64(0), None) == bad
+    assert L.inl_gdn_rule_fwd(*args, 2, 3, 64, 64, 0, None, ctypes.c_int64(0), None, None, ctypes.c_int64(0),
+                              None, ctypes.c_int64(0), None) == bad
+    # a stride shorter than a row
+    assert L.inl_gdn_rule_fwd(*args, 1, 1, 8, 8, 0, ctypes.c_void_p(16), ctypes.c_int64(8), ctypes.c_void_p(16),
+                              ctypes.c_void_p(16), ctypes.c_int64(0), ctypes.c_void_p(16), ctypes.c_int64(0),
+                              None) == bad
+    # gated norm: value_dim 129, core dtype neither f32 nor the model dtype
+    assert L.inl_gdn_gated_norm_fwd(ctypes.c_int64(4), 2, 129, 0, 0, None, ctypes.c_int64(0), None,
+                                    ctypes.c_int64(0), None, ctypes.c_float(1e-6), None, ctypes.c_int64(0), None) == bad
+    assert L.inl_gdn_gated_norm_fwd(ctypes.c_int64(4), 2, 64, 0, 1, None, ctypes.c_int64(0), None,
+                                    ctypes.c_int64(0), None, ctypes.c_float(1e-6), None, ctypes.c_int64(0), None) == bad
+    # inverse: size 65
+    assert L.inl_gdn_unit_lower_inverse_fwd(ctypes.c_int64(3), 65, None, None, None) == bad
+    assert L.inl_gdn_gates_fwd(ctypes.c_int64(4), 0, 0, None, ctypes.c_int64(0), None, ctypes.c_int64(0), None,
+                               None, None, None, None) == bad
+    assert "value_dim" in inl_hip.last_error() or "gdn" in inl_hip.last_error()

@@ -19,6 +19,7 @@ from pathlib import Path
 import numpy as np
 
 from oracle import attention as oa
+from oracle import gdn as ogdn
 from oracle import pooling as opool
 from oracle import prologue as opro
 
@@ -77,6 +78,18 @@ class OracleOps:
     def l2(self, x):
         return opool.l2_normalize(x)
 
+    def gdn_conv(self, x, cu, weight):
+        return ogdn.causal_conv(x, cu, weight)
+
+    def gdn_gates(self, a, b, dt_bias, neg_a):
+        return ogdn.gates(a, b, dt_bias, neg_a)
+
+    def gdn_rule(self, mixed, cu, nk, nv, dk, dv, g, beta):
+        return ogdn.rule_packed(mixed, cu, nk, nv, dk, dv, g, beta)
+
+    def gdn_gated_norm(self, core, z, weight, eps):
+        return ogdn.gated_norm(core, z, weight, eps)
+
 
 class HipOps:
     """The same ops through the HIP library in f32 (device tensors in and out
@@ -124,6 +137,24 @@ class HipOps:
 
     def l2(self, x):
         return self.inl.l2_normalize(self._t(x)).cpu().numpy().astype(np.float64)
+
+    def _cu(self, cu):
+        return self.torch.from_numpy(np.ascontiguousarray(cu, dtype=np.int32)).to(self.dev)
+
+    def gdn_conv(self, x, cu, weight):
+        return self.inl.gdn_conv(self._t(x), self._cu(cu), self._t(weight)).cpu().numpy().astype(np.float64)
+
+    def gdn_gates(self, a, b, dt_bias, neg_a):
+        g, beta = self.inl.gdn_gates(self._t(a), self._t(b), self._t(dt_bias), self._t(neg_a))
+        return g.cpu().numpy().astype(np.float64), beta.cpu().numpy().astype(np.float64)
+
+    def gdn_rule(self, mixed, cu, nk, nv, dk, dv, g, beta):
+        out = self.inl.gdn_rule(self._t(mixed), self._cu(cu), nk, nv, dk, dv, self._t(g), self._t(beta))
+        return out.cpu().numpy().astype(np.float64)
+
+    def gdn_gated_norm(self, core, z, weight, eps):
+        out = self.inl.gdn_gated_norm(self._t(core), self._t(z), self._t(weight), eps)
+        return out.cpu().numpy().astype(np.float64)
 
 
 def _positions(lens):
@@ -265,3 +296,106 @@ def modernbert_splade(fixture, rows, ops):
     dense = ops.splade(logits, ends, W["decoder.bias"].astype(np.float32), pool["logit_shift"],
                        pool["masked_vocab_ids"], pool["canonical_ids"])
     return [opool.sparse_from_pairs(row) for row in dense]
+
+
+# ---------------------------------------------------------------------------
+# Qwen3.5 late-interaction tower (crates/inl-late/src/qwen3_5.rs, native.rs)
+# ---------------------------------------------------------------------------
+
+def load_late_fixture(name: str = "tiny_qwen3_5_late"):
+    """(config, weights, golden, fixture dir, dense weight [out, hidden],
+    sentence-transformers prompts, lengths and mask config)."""
+    from safetensors.numpy import load_file
+    cfg, weights, golden, d = load_fixture(name)
+    dense = load_file(str(d / "dense.safetensors"))["linear.weight"].astype(np.float64)
+    st = {
+        "prompts": json.loads((d / "config_sentence_transformers.json").read_text())["prompts"],
+        "lengths": json.loads((d / "sentence_bert_config.json").read_text()),
+        "mask": json.loads((d / "mask_config.json").read_text()),
+        "dense": json.loads((d / "dense_config.json").read_text()),
+    }
+    return cfg, weights, golden, d, dense, st
+
+
+def _zero_centred_rms(x, weight, eps):
+    """Qwen3.5 RmsNorm: ``x / rms(x) * (1 + w)`` (qwen3_5.rs:189-210)."""
+    return opro.rms_norm(x, 1.0 + weight, eps)
+
+
+def qwen35_late_encode(fixture, texts, task: str, ops):
+    """Per-token unit vectors per text, following native.rs:281-311 (prompt
+    prepended, special tokens, cut to the task's length), qwen3_5.rs:893-910
+    (embedding, layers, final norm) with the layer of :788-799, the gated
+    delta net of :481-545 and the full attention of :302-348 (zero-centred
+    q/k RMSNorm, partial half-split RoPE on the first rotary_dim features,
+    bidirectional or causal per ``is_causal``, sigmoid output gate), then
+    native.rs:640-689 (the Dense projection, ``x / max(|x|, 1e-12)``, the
+    document skiplist). Rows are packed; the reference right pads them,
+    which leaves the real rows unchanged (qwen3_5.rs:1-7)."""
+    import tokenizers
+    cfg, W, _, fdir, dense, st = fixture
+    tc = cfg["text_config"]
+    length = min(st["lengths"][f"{task}_length"], tc["max_position_embeddings"])
+    tok = tokenizers.Tokenizer.from_file(str(fdir / "tokenizer.json"))
+    tok.no_truncation()
+    tok.no_padding()
+    ids = [tok.encode(st["prompts"][task] + t, add_special_tokens=True).ids[:length] for t in texts]
+    skip = []
+    if task in st["mask"].get("skiplist_tasks", []):
+        skip = [i for i in (tok.token_to_id(w) for w in st["mask"]["skiplist_words"]) if i is not None]
+    lens = [len(x) for x in ids]
+    cu = oa.cu_from_lengths(lens)
+    flat = np.concatenate([np.asarray(x, dtype=np.int64) for x in ids])
+    pos = _positions(lens)
+    n = flat.shape[0]
+    eps = tc["rms_norm_eps"]
+    p = "language_model."
+
+    def lin(x, name):
+        return x @ W[p + name + ".weight"].T
+
+    heads, kvh, hd = tc["num_attention_heads"], tc["num_key_value_heads"], tc["head_dim"]
+    rot = int(hd * tc["rope_parameters"].get("partial_rotary_factor", 1.0))
+    cos, sin = opro.rope_table_f32(rot, tc["rope_parameters"]["rope_theta"], max(lens))
+    nk, nv = tc["linear_num_key_heads"], tc["linear_num_value_heads"]
+    dk, dv = tc["linear_key_head_dim"], tc["linear_value_head_dim"]
+    h = W[p + "embed_tokens.weight"][flat]
+    for i, kind in enumerate(tc["layer_types"]):
+        lp = f"layers.{i}."
+        x = _zero_centred_rms(h, W[p + lp + "input_layernorm.weight"], eps)
+        if kind == "linear_attention":
+            a_ = lp + "linear_attn."
+            mixed = ops.gdn_conv(lin(x, a_ + "in_proj_qkv"), cu, W[p + a_ + "conv1d.weight"][:, 0, :])
+            neg_a = -np.exp(W[p + a_ + "A_log"])
+            g, beta = ops.gdn_gates(lin(x, a_ + "in_proj_a"), lin(x, a_ + "in_proj_b"), W[p + a_ + "dt_bias"], neg_a)
+            core = ops.gdn_rule(mixed, cu, nk, nv, dk, dv, g, beta)
+            z = lin(x, a_ + "in_proj_z").reshape(n, nv, dv)
+            y = ops.gdn_gated_norm(core, z, W[p + a_ + "norm.weight"], eps)
+            mix = lin(y.reshape(n, nv * dv), a_ + "out_proj")
+        else:
+            s_ = lp + "self_attn."
+            qg = lin(x, s_ + "q_proj").reshape(n, heads, 2 * hd)
+            q, gate = qg[..., :hd], qg[..., hd:].reshape(n, heads * hd)
+            q = _zero_centred_rms(q, W[p + s_ + "q_norm.weight"], eps)
+            k = _zero_centred_rms(lin(x, s_ + "k_proj").reshape(n, kvh, hd), W[p + s_ + "k_norm.weight"], eps)
+            v = lin(x, s_ + "v_proj").reshape(n, kvh, hd)
+            c, s = cos[pos][:, None, :].astype(np.float64), sin[pos][:, None, :].astype(np.float64)
+            q = opro.partial_rope(q, c, s, rot)
+            k = opro.partial_rope(k, c, s, rot)
+            a = ops.attention(q, k, v, cu, causal=bool(tc.get("is_causal", True)), window=-1, scale=hd ** -0.5)
+            a = a.reshape(n, heads * hd) * (1.0 / (1.0 + np.exp(-gate)))
+            mix = lin(a, s_ + "o_proj")
+        h = h + mix
+        m = _zero_centred_rms(h, W[p + lp + "post_attention_layernorm.weight"], eps)
+        m = lin(m, lp + "mlp.gate_proj")
+        m = (m / (1.0 + np.exp(-m))) * lin(_zero_centred_rms(h, W[p + lp + "post_attention_layernorm.weight"], eps),
+                                          lp + "mlp.up_proj")
+        h = h + lin(m, lp + "mlp.down_proj")
+    h = _zero_centred_rms(h, W[p + "norm.weight"], eps)
+    y = h @ dense.T
+    y = y / np.maximum(np.linalg.norm(y, axis=1, keepdims=True), 1e-12)
+    out = []
+    for b in range(len(ids)):
+        keep = [j for j, t in enumerate(ids[b]) if t not in skip]
+        out.append(y[cu[b] + np.asarray(keep, dtype=np.int64)] if keep else np.zeros((0, y.shape[1])))
+    return out, lens
