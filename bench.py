@@ -27,8 +27,11 @@ reference CPU flash path, timed on a bounded sample of the same workload.
 Other attention workloads (--workload): gemma_window, gemma_full,
 modernbert_local, modernbert_global, vision, pplx_causal, qwen3_2048,
 qwen3_2048_full - reported the same way. Op workloads (--workload norm_rope,
-pool_last, pool_mean, splade) time the prologue and epilogue kernels at
-their configurations' full sizes against the 8 TB/s HBM roofline. The
+pool_last, pool_mean, splade, gdn_conv, gdn_gated_norm) time the prologue,
+epilogue and gated-delta-net element-wise kernels at their configurations'
+full sizes against the 8 TB/s HBM roofline; splade_decoder (a GEMM) against
+the bf16 MFMA peak and gdn_rule (f32 vector work) against the 157.3 TFLOP/s
+fp32 vector peak. The
 end-to-end workloads (--workload qwen3_e2e, f32 as configuration 1, and
 qwen3_e2e_bf16) time a whole Qwen3-0.6B encode of 8 texts (778 tokens) and
 report encoded tokens/s, with the numpy f32 forward as the CPU baseline.
@@ -185,7 +188,14 @@ def roofline(tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch):
                       "frac": round(gbs / PEAK_HBM_GBS, 4)}}
 
 
-OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade", "splade_decoder")
+OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade", "splade_decoder", "gdn_conv", "gdn_rule",
+                "gdn_gated_norm")
+# What bounds each op workload that is not HBM-bound: the decoder is a GEMM
+# on the bf16 matrix cores; the delta rule is f32 vector (VALU) work, graded
+# against MI355X's 157.3 TFLOP/s fp32 vector peak (which counts packed-fp32
+# FMAs; this build disables packed fp32, so 78.6 TFLOP/s is its ceiling).
+OP_BOUND = {"splade_decoder": "mfma", "gdn_rule": "valu"}
+PEAK_FP32_TFLOPS = 157.3
 E2E_WORKLOADS = ("qwen3_e2e", "qwen3_e2e_bf16")
 PEAK_F32_TFLOPS = 157.3     # dense fp32 matrix peak
 
@@ -396,6 +406,36 @@ def op_workload(name, torch, inl_hip, dev):
                  f"(bf16, f32 accumulation) of 128 texts U[32,2048]; the {S * V * 4 / 1e9:.1f} GB of f32 logits "
                  "are never written")
         return label, "splade_decoder_max_kernel", 1, timed(launches), S, flops, "bf16"
+    if name.startswith("gdn_"):
+        # configuration 5's pplx-late linear-attention layer: 16 texts x 4096
+        # tokens, 16 key / 16 value heads of 128 (Qwen3.5-0.8B shape), conv 4
+        nk = nv = 16
+        dk = dv = 128
+        lens = [4096] * 16
+        cu = torch.tensor(w.cu_seqlens(lens), dtype=torch.int32, device=dev)
+        N, ch = sum(lens), 2 * nk * dk + nv * dv
+        shape = f"16 texts x 4096 tokens, {nk}/{nv} heads, dk = dv = {dk}, bf16"
+        if name == "gdn_conv":
+            proj = torch.randn(N, ch, generator=g, device=dev).to(torch.bfloat16)
+            wt = (torch.randn(ch, 4, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+            launches = [lambda: inl_hip.gdn_conv(proj, cu, wt, stream=stream)]
+            label = f"config5 gated-delta-net causal conv (4 taps) + silu over {ch} channels, {shape}"
+            return label, "gdn_conv_kernel", 1, timed(launches), N, N * ch * 2 * 2, "bf16"
+        mixed = torch.randn(N, ch, generator=g, device=dev).to(torch.bfloat16)
+        gg = -torch.rand(N, nv, generator=g, device=dev) * 0.2
+        beta = torch.rand(N, nv, generator=g, device=dev)
+        if name == "gdn_rule":
+            launches = [lambda: inl_hip.gdn_rule(mixed, cu, nk, nv, dk, dv, gg, beta, stream=stream)]
+            label = (f"config5 gated delta rule, f32 state per (text, head), {shape}; 7 dk dv flops per "
+                     "token and head (decay, S^T k, update, S^T q)")
+            return label, "gdn_rule_kernel", 1, timed(launches), N, 7 * N * nv * dk * dv, "f32"
+        if name == "gdn_gated_norm":
+            core = torch.randn(N, nv, dv, generator=g, device=dev)
+            z = torch.randn(N, nv, dv, generator=g, device=dev).to(torch.bfloat16)
+            nw = torch.ones(dv, device=dev).to(torch.bfloat16)
+            launches = [lambda: inl_hip.gdn_gated_norm(core, z, nw, 1e-6, stream=stream)]
+            label = f"config5 gated RMSNorm of the rule's f32 output with silu(z) gate, {shape}"
+            return label, "gdn_gated_norm_kernel", 1, timed(launches), N, N * nv * dv * (4 + 2 + 2), "bf16"
     raise SystemExit(f"unknown op workload {name}")
 
 
@@ -425,7 +465,8 @@ def op_main(args):
     import inl_hip
     dev = torch.device("cuda:0")
     label, kernel, n_launch, step, tokens, nbytes, dtype = op_workload(args.workload, torch, inl_hip, dev)
-    mfma = args.workload == "splade_decoder"   # a GEMM: its work is flops, not bytes
+    bound = OP_BOUND.get(args.workload, "hbm")
+    mfma = bound != "hbm"   # work counted in flops, not bytes
     log(f"workload: {label}; {nbytes / 1e9:.3f} {'GFLOP' if mfma else 'GB'} per step, {n_launch} launches")
     for _ in range(args.warmup):
         step()
@@ -439,15 +480,18 @@ def op_main(args):
     gbs = nbytes / n_launch / (avg_ms * 1e-3) / 1e9
     if mfma:
         tf = nbytes / n_launch / (avg_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic(args.workload), "kernel": kernel,
+        peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_FP32_TFLOPS
+        roof = {"bound": bound, "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(tf / peak, 4), "traffic": read_traffic(args.workload), "kernel": kernel,
                 "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"flop": nbytes / n_launch}}
     else:
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": read_traffic(args.workload), "kernel": kernel,
                 "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"hbm_bytes": nbytes / n_launch}}
     print(json.dumps({
-        "metric": f"{args.workload} op throughput ({'TFLOP/s vs bf16 MFMA peak' if mfma else 'HBM GB/s vs 8 TB/s'})",
+        "metric": f"{args.workload} op throughput ("
+                  + {"mfma": "TFLOP/s vs bf16 MFMA peak", "valu": "TFLOP/s vs fp32 vector peak",
+                     "hbm": "HBM GB/s vs 8 TB/s"}[bound] + ")",
         "value": round(tokens * args.steps / wall, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
