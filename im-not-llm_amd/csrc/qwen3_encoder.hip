@@ -18,9 +18,23 @@
 //
 // The attention schedule is planned once per call into the workspace and
 // reused by every layer; nothing is allocated per call.
+//
+// A call first uploads the batch (ids, positions, offsets, the attention
+// schedule) on the caller's stream, then issues the ~10 launches per layer.
+// At small batches those launches cost more host time than their kernels
+// take, so the launch sequence is kept as a HIP graph per batch shape: the
+// first call with a given (device, cu_seqlens, workspace, output) runs
+// eagerly, the second captures the sequence on a private stream and
+// instantiates it, and every call after that uploads the batch and launches
+// the graph on the caller's stream. The captured kernels read the batch from
+// the same workspace addresses, so the graph is valid for any ids of that
+// shape. A graph holding a memset node (a library call may record one) is
+// discarded and the encoder stays eager: such nodes are not replayed
+// reliably here.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -35,6 +49,16 @@ struct inl_qwen3 {
   float* final_norm_f32 = nullptr;  // device, owned
   float* cos = nullptr;             // device, owned: [max_positions, head_dim / 2]
   float* sin = nullptr;
+  // the launch-sequence graph of the last batch shape (see above)
+  std::mutex mu;
+  bool graphs = true;
+  int g_dev = -1;
+  std::vector<int32_t> g_cu;
+  void* g_ws = nullptr;
+  float* g_out = nullptr;
+  int g_runs = 0;                    // calls with this key so far
+  hipGraphExec_t g_exec = nullptr;
+  hipStream_t cap = nullptr;         // private capture stream (default priority)
 };
 
 namespace inl {
@@ -87,6 +111,69 @@ int layout(const inl_qwen3* e, int32_t n_texts, const int32_t* cu, Layout* L) {
   if (rc) return rc;
   L->gemm = take(gemm);
   L->total = off;
+  return INL_OK;
+}
+
+// The graph of `seq` for this batch key, or eager launches (see the file
+// comment). `seq(stream)` issues the whole launch sequence onto `stream`.
+template <typename Seq>
+int run_sequence(inl_qwen3* e, int32_t n_texts, const int32_t* cu, void* ws, float* out, hipStream_t st,
+                 Seq&& seq) {
+  std::lock_guard<std::mutex> g(e->mu);
+  if (!e->graphs) return seq((void*)st);
+  int dev = -1;
+  INL_HIP_TRY(hipGetDevice(&dev));
+  const bool same = dev == e->g_dev && ws == e->g_ws && out == e->g_out &&
+                    (int)e->g_cu.size() == n_texts + 1 && std::equal(cu, cu + n_texts + 1, e->g_cu.begin());
+  if (!same) {
+    if (e->g_exec) (void)hipGraphExecDestroy(e->g_exec);
+    e->g_exec = nullptr;
+    e->g_dev = dev;
+    e->g_ws = ws;
+    e->g_out = out;
+    e->g_cu.assign(cu, cu + n_texts + 1);
+    e->g_runs = 0;
+  }
+  if (e->g_exec) {
+    INL_HIP_TRY(hipGraphLaunch(e->g_exec, st));
+    return INL_OK;
+  }
+  if (e->g_runs++ == 0) return seq((void*)st);   // first call of a shape: eager
+  // second call: capture on the private stream, then launch on the caller's
+  if (!e->cap) INL_HIP_TRY(hipStreamCreateWithFlags(&e->cap, hipStreamNonBlocking));
+  INL_HIP_TRY(hipStreamBeginCapture(e->cap, hipStreamCaptureModeThreadLocal));
+  const int rc = seq((void*)e->cap);
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(e->cap, &graph);
+  if (rc) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+  }
+  if (end != hipSuccess || !graph) {
+    if (graph) (void)hipGraphDestroy(graph);
+    e->graphs = false;   // capture is not available here: stay eager
+    (void)hipGetLastError();
+    return seq((void*)st);
+  }
+  size_t n_nodes = 0;
+  hipError_t err = hipGraphGetNodes(graph, nullptr, &n_nodes);
+  std::vector<hipGraphNode_t> nodes(n_nodes);
+  if (err == hipSuccess && n_nodes) err = hipGraphGetNodes(graph, nodes.data(), &n_nodes);
+  bool memset = false;
+  for (size_t i = 0; err == hipSuccess && i < n_nodes; ++i) {
+    hipGraphNodeType t;
+    err = hipGraphNodeGetType(nodes[i], &t);
+    memset = memset || t == hipGraphNodeTypeMemset;
+  }
+  if (err == hipSuccess && !memset) err = hipGraphInstantiate(&e->g_exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (err != hipSuccess || memset || !e->g_exec) {
+    e->g_exec = nullptr;
+    e->graphs = false;
+    (void)hipGetLastError();
+    return seq((void*)st);
+  }
+  INL_HIP_TRY(hipGraphLaunch(e->g_exec, st));
   return INL_OK;
 }
 
@@ -160,9 +247,32 @@ extern "C" int inl_qwen3_create(const inl_qwen3_config* cfg, const void* embed_t
 
 extern "C" int inl_qwen3_destroy(inl_qwen3* e) {
   if (!e) return INL_OK;
+  if (e->g_exec) (void)hipGraphExecDestroy(e->g_exec);
+  if (e->cap) (void)hipStreamDestroy(e->cap);
   for (float* p : {e->cos, e->sin, e->final_norm_f32})
     if (p) (void)hipFree(p);
   delete e;
+  return INL_OK;
+}
+
+extern "C" int inl_qwen3_graph_info(inl_qwen3* e, int32_t* enabled, int32_t* held) {
+  using namespace inl;
+  if (!e || !enabled || !held) return fail(INL_E_INVALID, "qwen3: bad arguments");
+  std::lock_guard<std::mutex> g(e->mu);
+  *enabled = e->graphs ? 1 : 0;
+  *held = e->g_exec ? 1 : 0;
+  return INL_OK;
+}
+
+extern "C" int inl_qwen3_set_graphs(inl_qwen3* e, int32_t enable) {
+  using namespace inl;
+  if (!e) return fail(INL_E_INVALID, "qwen3: encoder is NULL");
+  std::lock_guard<std::mutex> g(e->mu);
+  e->graphs = enable != 0;
+  if (e->g_exec) (void)hipGraphExecDestroy(e->g_exec);
+  e->g_exec = nullptr;
+  e->g_runs = 0;
+  e->g_cu.clear();
   return INL_OK;
 }
 
@@ -249,6 +359,8 @@ extern "C" int inl_qwen3_encode(inl_qwen3* e, int32_t n_texts, const int32_t* cu
   rc = inl_attn_plan_create_in(&ad, ws + L.sched, L.gemm - L.sched, stream, &plan);
   if (rc) return rc;
 
+  // the launch sequence, onto stream `sq` (the caller's, or the capture stream)
+  auto sequence = [&](void* sq) -> int {
   inl_norm_rope_desc nr{};
   nr.n_tokens = n;
   nr.head_dim = c.head_dim;
@@ -262,7 +374,8 @@ extern "C" int inl_qwen3_encode(inl_qwen3* e, int32_t n_texts, const int32_t* cu
   // in bf16 the reference keeps its tables and the normed q/k in bf16
   nr.round_tables = nr.round_norm = dt == INL_BF16;
 
-  rc = inl_embed_fwd(n, d_ids, e->embed, c.vocab, c.hidden, dt, resid, c.hidden, stream);
+  void* stream = sq;
+  int rc = inl_embed_fwd(n, d_ids, e->embed, c.vocab, c.hidden, dt, resid, c.hidden, stream);
   for (int i = 0; i < c.layers && !rc; ++i) {
     const inl_qwen3_layer_weights& w = e->layers[i];
     rc = inl_rms_norm_rows_fwd(n, c.hidden, resid, c.hidden, w.input_norm, dt, c.eps, dt, x, c.hidden, stream);
@@ -290,6 +403,10 @@ extern "C" int inl_qwen3_encode(inl_qwen3* e, int32_t n_texts, const int32_t* cu
   }
   if (!rc) rc = inl_pool_last_fwd(n_texts, d_cu, c.hidden, c.hidden, INL_F32, resid, e->final_norm_f32, c.eps, 0,
                                   out, stream);
+  return rc;
+  };
+
+  rc = run_sequence(e, n_texts, cu, workspace, out, st, sequence);
   const int rc2 = inl_attn_plan_destroy(plan);
   return rc ? rc : rc2;
 }

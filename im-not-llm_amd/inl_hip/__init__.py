@@ -518,6 +518,8 @@ _q3_create = _sig("inl_qwen3_create", ctypes.c_int, ctypes.POINTER(Qwen3Config),
                   ctypes.POINTER(Qwen3LayerWeights), c_void_p, ctypes.POINTER(c_void_p))
 _q3_destroy = _sig("inl_qwen3_destroy", ctypes.c_int, c_void_p)
 _q3_ws = _sig("inl_qwen3_workspace_size", ctypes.c_int, c_void_p, c_i32, c_void_p, ctypes.POINTER(ctypes.c_size_t))
+_q3_graphs = _sig("inl_qwen3_set_graphs", ctypes.c_int, c_void_p, c_i32)
+_q3_ginfo = _sig("inl_qwen3_graph_info", ctypes.c_int, c_void_p, ctypes.POINTER(c_i32), ctypes.POINTER(c_i32))
 _q3_encode = _sig("inl_qwen3_encode", ctypes.c_int, c_void_p, c_i32, c_void_p, c_void_p, c_void_p, c_void_p,
                   ctypes.c_size_t, c_void_p)
 
@@ -631,6 +633,17 @@ class Qwen3Encoder:
         _check(_q3_ws(self._h, len(cu_seqlens) - 1, cu, ctypes.byref(n)))
         return n.value
 
+    def set_graphs(self, enable: bool) -> None:
+        """``inl_qwen3_set_graphs``: keep (True, the default) or stop keeping
+        the launch sequence of a batch shape as a HIP graph."""
+        _check(_q3_graphs(self._h, 1 if enable else 0))
+
+    def graph_info(self):
+        """(graphs enabled, a graph of the last batch shape is held)."""
+        en, held = c_i32(), c_i32()
+        _check(_q3_ginfo(self._h, ctypes.byref(en), ctypes.byref(held)))
+        return bool(en.value), bool(held.value)
+
     def encode(self, ids, cu_seqlens, *, out=None, workspace=None, stream=None):
         """``ids``: host int sequence of the packed token ids; returns f32
         ``[texts, hidden]`` unit vectors on the device."""
@@ -645,7 +658,9 @@ class Qwen3Encoder:
         if out is None:
             out = torch.empty((nt, self.cfg.hidden), dtype=torch.float32, device=dev)
         need = self.workspace_bytes(cu_seqlens)
-        if workspace is None or workspace.numel() < need:
+        if workspace is None:   # reuse the last one: same addresses let a batch shape keep its graph
+            workspace = getattr(self, "_last_ws", None)
+        if workspace is None or workspace.numel() < need + 256:
             workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
         ptr = workspace.data_ptr()
         ptr += (-ptr) % 256

@@ -145,11 +145,27 @@ int inl_qwen3_workspace_size(const inl_qwen3* enc, int32_t n_texts,
  * RMSNorm of text b's last row (+1e-12 inside the square root,
  * qwen3/mod.rs:468). ids_host: [cu_seqlens_host[n_texts]] token ids, checked
  * against vocab on the host. Texts of length 0 are refused, as the
- * reference refuses an empty tokenisation (qwen3/mod.rs:446-448). */
+ * reference refuses an empty tokenisation (qwen3/mod.rs:446-448).
+ * The batch is uploaded with pageable copies on `stream`, then the layers
+ * run. With graphs on (the default), the launch sequence of a batch shape -
+ * the same device, cu_seqlens_host, workspace and embeddings pointer - is
+ * captured on its second call and replayed from the third on (the first
+ * runs eagerly). Calls on one encoder are serialised by a lock; the
+ * encoder keeps the graph of one shape at a time. */
 int inl_qwen3_encode(inl_qwen3* enc, int32_t n_texts,
                      const int32_t* cu_seqlens_host, const int32_t* ids_host,
                      float* embeddings, void* workspace, size_t workspace_bytes,
                      void* stream);
+
+/* Turns the launch-sequence graph of inl_qwen3_encode on (enable != 0, the
+ * default) or off, and drops the graph held. No counterpart in the
+ * reference, whose candle forward issues every op eagerly. */
+int inl_qwen3_set_graphs(inl_qwen3* enc, int32_t enable);
+/* *enabled: graphs are on (they turn off by themselves if capture is not
+ * possible or a captured graph holds a memset); *held: a graph of the last
+ * batch shape is instantiated and will be launched by the next call of
+ * that shape. */
+int inl_qwen3_graph_info(inl_qwen3* enc, int32_t* enabled, int32_t* held);
 
 #ifdef __cplusplus
 }

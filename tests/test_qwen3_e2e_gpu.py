@@ -92,3 +92,41 @@ def test_runner_refuses_bad_inputs(cuda, inl):
     torch.cuda.synchronize()
     assert np.isfinite(out.cpu().numpy()).all()
     enc.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_graph_replays_match_eager(dtype, cuda, inl):
+    """The runner's launch-sequence graph (captured on a shape's second call,
+    replayed after) gives bit-identical embeddings to eager launches, for
+    new ids on every call, with eager work of another encoder and
+    synchronisations between the replays; a new shape drops the graph and
+    the first shape builds it again."""
+    import torch
+    cfg = oq.Qwen3Config(vocab=2048, layers=2)
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    wd = _to_device(oq.random_weights(cfg, seed=3), torch, cuda, td)
+    eager = inl.Qwen3Encoder(cfg, wd, max_positions=256)
+    eager.set_graphs(False)
+    graph = inl.Qwen3Encoder(cfg, wd, max_positions=256)
+    rng = np.random.default_rng(7)
+
+    def run(lengths, calls):
+        cu = oa.cu_from_lengths(lengths).tolist()
+        out = torch.empty((len(lengths), cfg.hidden), dtype=torch.float32, device=cuda)
+        ws = torch.empty(graph.workspace_bytes(cu) + 256, dtype=torch.uint8, device=cuda)
+        for i in range(calls):
+            ids = rng.integers(0, cfg.vocab, sum(lengths))
+            got = graph.encode(ids, cu, out=out, workspace=ws).clone()
+            want = eager.encode(ids, cu)
+            torch.cuda.synchronize()
+            held = graph.graph_info()
+            print(f"{dtype} {lengths} call {i}: graph info {held}", flush=True)
+            assert torch.equal(got, want), f"call {i} differs by {(got - want).abs().max().item():.3g}"
+            if i >= 1:
+                assert held == (True, True), "the second call of a shape should leave a graph held"
+
+    run([1, 17, 200, 64, 129, 3], 5)
+    run([5, 40], 3)
+    run([1, 17, 200, 64, 129, 3], 3)
+    eager.close()
+    graph.close()
