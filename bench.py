@@ -26,7 +26,9 @@ reference CPU flash path, timed on a bounded sample of the same workload.
 
 Other attention workloads (--workload): gemma_window, gemma_full,
 modernbert_local, modernbert_global, vision, pplx_causal, qwen3_2048,
-qwen3_2048_full - reported the same way. Op workloads (--workload norm_rope,
+qwen3_2048_full - reported the same way, and each of them in f32 with an
+`_f32` suffix (e.g. `qwen3_f32`: the f32 kernel against the 157.3 TFLOP/s
+fp32 matrix peak). Op workloads (--workload norm_rope,
 pool_last, pool_mean, splade, gdn_conv, gdn_gated_norm) time the prologue,
 epilogue and gated-delta-net element-wise kernels at their configurations'
 full sizes against the 8 TB/s HBM roofline; splade_decoder (a GEMM) against
@@ -95,9 +97,11 @@ def workload(name: str):
     raise SystemExit(f"unknown workload {name}")
 
 
-def make_inputs(lengths, hq, hkv, d, scale, seed, torch, dev):
+def make_inputs(lengths, hq, hkv, d, scale, seed, torch, dev, dtype=None):
     """Seeded N(0,1) q/k/v through an RMSNorm with weights 1 + 0.2 u (u in
-    [-0.5, 0.5)), q scaled so that scale * q.k has unit variance; bf16."""
+    [-0.5, 0.5)), q scaled so that scale * q.k has unit variance; bf16
+    unless `dtype` says otherwise."""
+    dtype = dtype or torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(seed)
     n = int(sum(lengths))
 
@@ -105,7 +109,7 @@ def make_inputs(lengths, hq, hkv, d, scale, seed, torch, dev):
         x = torch.randn(n, h, d, generator=g, device=dev)
         w = 1.0 + 0.2 * (torch.rand(d, generator=g, device=dev) - 0.5)
         x = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6) * w
-        return (x * s).to(torch.bfloat16)
+        return (x * s).to(dtype)
 
     q = normed(hq, d ** -0.5 / scale)
     k = normed(hkv, 1.0)
@@ -172,15 +176,16 @@ def cpu_model() -> str:
     return f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, model {info.get('model', '?')})"
 
 
-def roofline(tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch):
-    """The attention kernel against the bf16 dense MFMA peak (attention is a
-    dense contraction and is graded on matrix-core use), with its HBM
-    bandwidth beside it under ``other``; ``hbm_floor_exceeds_mfma_floor``
-    says when the launch's bytes, not its flops, set the lower bound on time."""
-    mfma_floor = flop_launch / (PEAK_BF16_TFLOPS * 1e12)
+def roofline(tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch, peak=PEAK_BF16_TFLOPS):
+    """The attention kernel against the dense MFMA peak of its dtype (bf16
+    2516.6, f32 157.3 TFLOP/s: attention is a dense contraction and is
+    graded on matrix-core use), with its HBM bandwidth beside it under
+    ``other``; ``hbm_floor_exceeds_mfma_floor`` says when the launch's
+    bytes, not its flops, set the lower bound on time."""
+    mfma_floor = flop_launch / (peak * 1e12)
     hbm_floor = bytes_launch / (PEAK_HBM_GBS * 1e9)
-    return {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+    return {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(tflops / peak, 4), "traffic": traffic,
             "kernel": kernel, "avg_launch_us": round(avg_ms * 1e3, 2),
             "algorithmic_per_launch": {"flop": flop_launch, "hbm_bytes": bytes_launch},
             "hbm_floor_exceeds_mfma_floor": hbm_floor > mfma_floor,
@@ -542,19 +547,27 @@ def main():
     from inl_hip import attention_flops
 
     dev = torch.device("cuda:0")
-    batches, hq, hkv, d, causal, window, scale, label = workload(args.workload)
-    inputs = [make_inputs(lens, hq, hkv, d, scale, 1000 + i, torch, dev) for i, lens in enumerate(batches)]
+    # "<workload>_f32": the same shapes in f32 (configuration 1's dtype), on the
+    # f32 kernel, graded against the 157.3 TFLOP/s fp32 matrix peak
+    f32 = args.workload.endswith("_f32")
+    base = args.workload[:-4] if f32 else args.workload
+    dt_name, td, es = ("f32", torch.float32, 4) if f32 else ("bf16", torch.bfloat16, 2)
+    peak = PEAK_F32_TFLOPS if f32 else PEAK_BF16_TFLOPS
+    batches, hq, hkv, d, causal, window, scale, label = workload(base)
+    if f32:
+        label = label.replace("bf16", "f32")
+    inputs = [make_inputs(lens, hq, hkv, d, scale, 1000 + i, torch, dev, td) for i, lens in enumerate(batches)]
     plans, outs = [], []
     for lens, (q, k, v) in zip(batches, inputs):
         cu = inl_hip.workloads.cu_seqlens(lens)
         desc = inl_hip.make_attn_desc(cu, hq, hkv, d, causal=causal, window=window, scale=scale,
-                                      dtype="bf16", out_dtype="bf16")
+                                      dtype=dt_name, out_dtype=dt_name)
         plans.append(inl_hip.AttnPlan(desc))
         outs.append(torch.empty_like(q))
     tokens = sum(sum(b) for b in batches)
     flops = sum(attention_flops(b, hq, d, causal, window) for b in batches)
-    # algorithmic HBM bytes: Q, K, V read once and O written once, bf16
-    hbm_bytes = tokens * (2 * hq * d + 2 * 2 * hkv * d + 2 * hq * d)
+    # algorithmic HBM bytes: Q, K, V read once and O written once
+    hbm_bytes = tokens * (hq * d + 2 * hkv * d + hq * d) * es
     kernel = inl_hip.kernel_name(plans[0].desc)
     n_launch = len(batches)
     stream = torch.cuda.current_stream()
@@ -599,7 +612,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": dt_name,
         "data": "synthetic (seeded N(0,1) q/k/v after RMSNorm; no checkpoint)",
         "config": {"workload": label, "tokens_per_step": tokens, "launches_per_step": n_launch,
                    "attention_tflop_per_step": round(flops / 1e12, 6),
@@ -607,9 +620,9 @@ def main():
                                 "second (a step runs the op once over every batch), not end-to-end "
                                 "encoded tokens/s")},
         "attention_tflops": round(flops * args.steps / wall / 1e12, 2),
-        "attention_frac_of_peak": round(flops * args.steps / wall / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "attention_frac_of_peak": round(flops * args.steps / wall / 1e12 / peak, 4),
         "roofline": roofline(achieved, achieved_gbs, traffic, kernel, avg_launch_ms, flops / n_launch,
-                             hbm_bytes / n_launch),
+                             hbm_bytes / n_launch, peak),
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale,
