@@ -44,29 +44,54 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const ch
 
 // ---- RMSNorm of f32 rows into TO: one wave per row ----
 // y = x / sqrt(mean(x^2) + eps) * w (w in TW, the model dtype). Each lane
-// sums its 4-float chunks of the row; 64-lane xor-shuffle reduction.
-template <typename TW, typename TO>
+// sums its 4-float chunks of the row; 64-lane xor-shuffle reduction. With
+// K > 0 the row (at most K * 256 values) stays in registers between the two
+// passes: K loads per lane issued at once from clamped addresses (masked
+// after, so no load waits behind a branch), the row read once. K = 0 reads
+// a longer row twice.
+template <typename TW, typename TO, int K>
 __global__ __launch_bounds__(256) void rms_rows_kernel(const float* x, int64_t xs, int64_t rows, int32_t dim,
                                                        const char* w, float eps, char* y, int64_t ys) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= rows) return;
   const float* xr = x + r * xs;
-  float ss = 0.f;
-  for (int i = lane * 4; i < dim; i += 256) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(xr + i);
-    ss += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
-  }
-  for (int m = 32; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
-  const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
   char* yr = y + r * ys * (int64_t)sizeof(TO);
-  for (int i = lane * 4; i < dim; i += 256) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(xr + i);
+  auto put = [&](int i, const f32x4& v, float inv) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float wv = w ? ldf<TW>(w + (i + e) * (int)sizeof(TW)) : 1.f;
       stf<TO>(yr + (i + e) * (int)sizeof(TO), v[e] * inv * wv);
     }
+  };
+  float ss = 0.f;
+  if constexpr (K > 0) {
+    f32x4 held[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int i = lane * 4 + 256 * k;
+      held[k] = *reinterpret_cast<const f32x4*>(xr + (i < dim ? i : dim - 4));
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (lane * 4 + 256 * k >= dim) held[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      ss += (held[k][0] * held[k][0] + held[k][1] * held[k][1]) + (held[k][2] * held[k][2] + held[k][3] * held[k][3]);
+    }
+    for (int m = 32; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int i = lane * 4 + 256 * k;
+      if (i < dim) put(i, held[k], inv);
+    }
+  } else {
+    for (int i = lane * 4; i < dim; i += 256) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(xr + i);
+      ss += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+    }
+    for (int m = 32; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = lane * 4; i < dim; i += 256) put(i, *reinterpret_cast<const f32x4*>(xr + i), inv);
   }
 }
 
@@ -155,14 +180,24 @@ extern "C" int inl_rms_norm_rows_fwd(int64_t rows, int32_t dim, const float* x, 
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)((rows + 3) / 4));
   const char* w = (const char*)weight;
-  if (weight_dtype == INL_BF16 && out_dtype == INL_BF16)
-    hipLaunchKernelGGL((rms_rows_kernel<bf16, bf16>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys);
-  else if (weight_dtype == INL_BF16)
-    hipLaunchKernelGGL((rms_rows_kernel<bf16, float>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys);
-  else if (out_dtype == INL_BF16)
-    hipLaunchKernelGGL((rms_rows_kernel<float, bf16>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys);
-  else
-    hipLaunchKernelGGL((rms_rows_kernel<float, float>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys);
+  // chunks of 256 values a lane holds: the smallest of 1, 2, 4, 8 that covers
+  // the row, 0 (two passes) beyond 2048
+  const int K = dim <= 256 ? 1 : dim <= 512 ? 2 : dim <= 1024 ? 4 : dim <= 2048 ? 8 : 0;
+  auto launch = [&](auto tw, auto to) {
+    using TW = decltype(tw);
+    using TO = decltype(to);
+    switch (K) {
+      case 1: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 1>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
+      case 2: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 2>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
+      case 4: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 4>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
+      case 8: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 8>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
+      default: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 0>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys);
+    }
+  };
+  if (weight_dtype == INL_BF16 && out_dtype == INL_BF16) launch(bf16{}, bf16{});
+  else if (weight_dtype == INL_BF16) launch(bf16{}, float{});
+  else if (out_dtype == INL_BF16) launch(float{}, bf16{});
+  else launch(float{}, float{});
   INL_HIP_TRY(hipGetLastError());
   return INL_OK;
 }

@@ -98,6 +98,19 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
   const bool valid = tok < (uint32_t)p.n_tokens;
   const int heads = min(p.heads, hfirst + HB);
 
+  // Every load below is issued unconditionally from a valid address and
+  // masked afterwards: a load under a per-lane condition becomes a branch
+  // that waits for it, which would put the x rows, the position and the
+  // table row one after another instead of in flight together. x goes first.
+  const uint32_t tokc = valid ? tok : 0u;   // launches have n_tokens >= 1
+  const char* xt = p.x + ((int64_t)tokc * p.x_stride + 8 * j) * (int64_t)sizeof(TI);
+  char* yt = p.y + ((int64_t)tok * p.y_stride + 8 * j) * (int64_t)sizeof(TO);
+  const int64_t hstep_x = (int64_t)p.head_dim * (int64_t)sizeof(TI);
+  const int64_t hstep_y = (int64_t)p.head_dim * (int64_t)sizeof(TO);
+  float v[HB][8];
+#pragma unroll
+  for (int i = 0; i < HB; ++i) load8<TI>(xt + min(hfirst + i, heads - 1) * hstep_x, v[i]);
+
   // ---- per-token constants ----
   float w[8];
 #pragma unroll
@@ -112,10 +125,10 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) { c[e] = 1.f; sn[e] = 0.f; }
   bool bad_pos = false;
+  int sec_lanes = 0, sec0 = 0;
   if (p.rotary_dim == 8 && p.sections == 1) {
     mode = j == 0 ? 1 : 0;
   } else if (p.rotary_dim > 0) {
-    int sec_lanes, sec0;  // lanes per rotated section, first lane of it
     if (p.sections == 2) {
       sec_lanes = G >> 1;
       sec0 = j < sec_lanes ? 0 : sec_lanes;
@@ -131,45 +144,43 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
       partner = lane + (first ? half_lanes : -half_lanes);
     }
   }
-  if (mode != 0 && valid) {
-    const int32_t pos = p.rows[tok];
-    if (pos < 0 || pos >= p.table_rows) {
-      bad_pos = true;
-    } else if (mode == 1) {
-      const f32x4 c4 = *reinterpret_cast<const f32x4*>(p.cos + (int64_t)pos * 4);
-      const f32x4 s4 = *reinterpret_cast<const f32x4*>(p.sin + (int64_t)pos * 4);
+  if (p.rotary_dim > 0) {   // uniform: the tables exist
+    const int32_t pos = p.rows[tokc];
+    bad_pos = mode != 0 && valid && (pos < 0 || pos >= p.table_rows);
+    const int64_t posc = pos < 0 ? 0 : (pos >= p.table_rows ? p.table_rows - 1 : pos);
+    float tc[8], ts[8];
+    if (p.rotary_dim == 8 && p.sections == 1) {
+      const f32x4 c4 = *reinterpret_cast<const f32x4*>(p.cos + posc * 4);
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(p.sin + posc * 4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) { c[e] = c4[e]; sn[e] = s4[e]; }
+      for (int e = 0; e < 4; ++e) { tc[e] = c4[e]; ts[e] = s4[e]; tc[e + 4] = 1.f; ts[e + 4] = 0.f; }
     } else {
-      int sec_lanes = p.sections == 2 ? G >> 1 : p.rotary_dim >> 3;
       const int half_lanes = sec_lanes >> 1;
       const int width = half_lanes * 8;              // table columns
       const bool second_sec = p.sections == 2 && !(j < (G >> 1));
       const float* ct = second_sec ? p.cos2 : p.cos;
       const float* st = second_sec ? p.sin2 : p.sin;
       const int jj = j - (second_sec ? (G >> 1) : 0);
-      const int col = 8 * (first ? jj : jj - half_lanes);
-      load8<float>(reinterpret_cast<const char*>(ct + (int64_t)pos * width + col), c);
-      load8<float>(reinterpret_cast<const char*>(st + (int64_t)pos * width + col), sn);
+      const int col = mode == 2 ? 8 * (first ? jj : jj - half_lanes) : 0;
+      load8<float>(reinterpret_cast<const char*>(ct + posc * width + col), tc);
+      load8<float>(reinterpret_cast<const char*>(st + posc * width + col), ts);
     }
-    if (p.round_tables)
+    if (mode != 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) { c[e] = round_bf16(c[e]); sn[e] = round_bf16(sn[e]); }
+      for (int e = 0; e < 8; ++e) { c[e] = tc[e]; sn[e] = ts[e]; }
+      if (p.round_tables)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { c[e] = round_bf16(c[e]); sn[e] = round_bf16(sn[e]); }
+    }
   }
 
-  const char* xt = p.x + ((int64_t)tok * p.x_stride + 8 * j) * (int64_t)sizeof(TI);
-  char* yt = p.y + ((int64_t)tok * p.y_stride + 8 * j) * (int64_t)sizeof(TO);
-  const int64_t hstep_x = (int64_t)p.head_dim * (int64_t)sizeof(TI);
-  const int64_t hstep_y = (int64_t)p.head_dim * (int64_t)sizeof(TO);
-  for (int h0 = hfirst; h0 < heads; h0 += HB) {   // one step
-    float v[HB][8];
 #pragma unroll
-    for (int i = 0; i < HB; ++i) {
-      if (valid && h0 + i < heads) load8<TI>(xt + (h0 + i) * hstep_x, v[i]);
-      else
+  for (int i = 0; i < HB; ++i)
+    if (!(valid && hfirst + i < heads))
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
-    }
+      for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+  {
+    const int h0 = hfirst;   // this lane group's one step of HB heads
 #pragma unroll
     for (int i = 0; i < HB; ++i) {
       if (p.norm) {
