@@ -45,6 +45,29 @@ EXTRA = {
     "attn_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
+# Sources whose kernels issue global loads from inline asm and wait for them
+# with hand-counted `s_waitcnt vmcnt`: the compiler believes an asm load's
+# destination register is written when the asm statement ends, so a register
+# spill could store that register, or hand it to another value, while the
+# load is still in flight. Their kernels must use no scratch; the build reads
+# the compiler's resource-usage remarks and fails if any of them does.
+NO_SCRATCH = {"attn_pp.hip", "attn_pp64.hip", "attn_wide.hip", "splade_decoder.hip"}
+RESOURCE_REMARKS = ["-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"]
+
+
+def scratch_users(remarks: str) -> list[str]:
+    """Kernels that the compiler's kernel-resource-usage remarks report with
+    a nonzero ScratchSize (bytes per lane)."""
+    users, name = [], None
+    for line in remarks.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:", 1)[1].split()[0]
+        elif "ScratchSize [bytes/lane]:" in line:
+            size = int(line.split("ScratchSize [bytes/lane]:", 1)[1].split()[0])
+            if size and name:
+                users.append(f"{name} ({size} B/lane)")
+    return users
+
 
 def sources():
     return sorted(CSRC.glob("*.hip"))
@@ -66,13 +89,20 @@ def build(verbose: bool = False) -> Path:
         jobs = []
         for src in sources():
             obj = Path(objdir) / (src.stem + ".o")
-            cmd = [HIPCC, *FLAGS, "-c", *EXTRA.get(src.name, []), str(src), "-o", str(obj)]
+            cmd = [HIPCC, *FLAGS, "-c", *EXTRA.get(src.name, []),
+                   *(RESOURCE_REMARKS if src.name in NO_SCRATCH else []), str(src), "-o", str(obj)]
             jobs.append((src, obj, cmd))
         with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1, 8)) as pool:
             results = list(pool.map(lambda j: _run(j[2]), jobs))
         for (src, _, _), (rc, err) in zip(jobs, results):
             if rc != 0:
                 raise RuntimeError(f"hipcc failed on {src.name} ({rc}):\n{err}")
+            if src.name in NO_SCRATCH:
+                users = scratch_users(err)
+                if users:
+                    raise RuntimeError(f"{src.name}: kernels with inline-asm loads use scratch: "
+                                       + ", ".join(users))
+                err = "\n".join(l for l in err.splitlines() if "kernel-resource-usage" not in l)
             if verbose and err.strip():
                 print(err, file=sys.stderr)
         rc, err = _run([HIPCC, *LINK_FLAGS, *(str(o) for _, o, _ in jobs), "-o", str(tmp)])

@@ -177,3 +177,24 @@ def test_gdn_entry_points_validate_on_the_host():
     assert L.inl_gdn_gates_fwd(ctypes.c_int64(4), 0, 0, None, ctypes.c_int64(0), None, ctypes.c_int64(0), None,
                                None, None, None, None) == bad
     assert "value_dim" in inl_hip.last_error() or "gdn" in inl_hip.last_error()
+
+
+def test_asm_load_kernels_use_no_scratch():
+    """Kernels that issue global loads from inline asm must compile without
+    scratch: the build reads the compiler's resource remarks for them and
+    fails on a spill. Checks the parser on the remark text the compiler
+    prints, and that those sources are the ones with inline-asm loads."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("inl_build", ROOT / "im-not-llm_amd" / "build.py")
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    text = ("x.hip:62:1: remark: Function Name: _Z1kv [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:62:1: remark:     VGPRs: 237 [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:62:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:90:1: remark: Function Name: _Z1jv [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:90:1: remark:     ScratchSize [bytes/lane]: 284 [-Rpass-analysis=kernel-resource-usage]\n")
+    assert b.scratch_users(text) == ["_Z1jv (284 B/lane)"]
+    asm_loads = {p.name for p in (ROOT / "im-not-llm_amd" / "csrc").glob("*.hip")
+                 if re.search(r'asm volatile\("buffer_load', p.read_text())
+                 or re.search(r'vmcnt\(%', p.read_text()) or '"attn_stream.hpp"' in p.read_text()}
+    assert asm_loads <= b.NO_SCRATCH, asm_loads - b.NO_SCRATCH
