@@ -388,6 +388,27 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
   // ---- epilogue: O = O^T / l, one query row per lane column ----
   if (!active || !qvalid) return;
   const float l_tot = half_sum(l_i);
+  const int part = p.item_part ? p.item_part[item_idx] : -1;
+  if (part >= 0) {
+    // Part of the block's key range: unnormalised O with its row max and
+    // sum, 32 rows of D floats per wave and head group.
+    const int64_t slot = ((int64_t)part * p.n_hg + hg) * NW + wave;
+    float* prow = p.part_o + (slot * 32 + lq) * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + 8 * g + 4 * hf;
+        if (d0 < hd) {
+          f32x4 val;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e];
+          *reinterpret_cast<f32x4*>(prow + d0) = val;
+        }
+      }
+    if (hf == 0) p.part_ml[slot * 32 + lq] = make_float2(m_i, l_tot);
+    return;
+  }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   char* orow = p.o + ((int64_t)(seg + qrow) * p.o_stride + (int64_t)head * hd) * (p.out_bf16 ? 2 : 4);
 #pragma unroll
@@ -407,6 +428,114 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
           for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e] * inv;
           *reinterpret_cast<f32x4*>(orow + d0 * 4) = val;
         }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Merge of a split key range. A query block whose key tiles were split over
+// several items has one partial slot per part (consecutive, from `first`);
+// row r's output is sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M the
+// largest m_s (parts in which the row saw no key have m_s = -inf, weight 0).
+// One workgroup per (block, head group, wave of the attention kernel, half):
+// 16 rows of 16 threads, each thread up to 4 chunks of 4 dims (head_dim <=
+// 256). Parts are taken 4 at a time, all their loads issued before any is
+// used, with a running max and rescale between groups.
+// ---------------------------------------------------------------------------
+
+struct MergeParams {
+  const int4* blocks;     // {seg_start, seg_len, q0, first partial slot}
+  const int32_t* n_parts; // parts per block
+  const float* part_o;
+  const float2* part_ml;
+  char* o;
+  int64_t o_stride;
+  int32_t n_hg, nw, rb, hpw, group, groups_per_kv, head_dim, dpad, out_bf16;
+};
+
+constexpr int kMergeThreads = 256;
+constexpr int kMergeTpr = 16;                           // threads per row
+constexpr int kMergeRows = kMergeThreads / kMergeTpr;   // rows per workgroup
+constexpr int kMergeWgPerWave = 32 / kMergeRows;
+
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(MergeParams p) {
+  constexpr int CPT = 256 / 4 / kMergeTpr;  // chunks per thread at head_dim 256
+  constexpr int G = 4;                      // parts per group
+  const int half = blockIdx.x % kMergeWgPerWave;
+  const int w = (blockIdx.x / kMergeWgPerWave) % p.nw;
+  const int bh = blockIdx.x / kMergeWgPerWave / p.nw;
+  const int bi = bh / p.n_hg;
+  const int hg = bh - bi * p.n_hg;
+  const int4 blk = p.blocks[bi];
+  const int ns = p.n_parts[bi];
+  const int kvh = hg / p.groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * p.groups_per_kv) * p.hpw + w / p.rb;
+  const int r = half * kMergeRows + threadIdx.x / kMergeTpr;  // row within the wave's 32
+  const int sub = threadIdx.x % kMergeTpr;
+  const int row = blk.z + (w % p.rb) * 32 + r;
+  if (row >= blk.y) return;
+  const int chunks = p.head_dim / 4;
+  // part s of this wave's rows: slot (first + s) * n_hg * nw + hg * nw + w
+  const int64_t slot0 = ((int64_t)blk.w * p.n_hg + hg) * p.nw + w;
+  const int64_t sstep = (int64_t)p.n_hg * p.nw * 32;  // rows between parts
+  const float2* ml = p.part_ml + slot0 * 32 + r;
+  const float* po = p.part_o + (slot0 * 32 + r) * p.dpad;
+  float mx = -INFINITY, l = 0.f;
+  f32x4 acc[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < ns; s0 += G) {
+    float2 m[G];
+    f32x4 v[G][CPT];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int s = min(s0 + g, ns - 1);  // past the end: re-read the last part, weight 0
+      m[g] = ml[s * sstep];
+      const float* ps = po + s * sstep * p.dpad;
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        const int c = min(sub + kMergeTpr * j, chunks - 1);
+        v[g][j] = *reinterpret_cast<const f32x4*>(ps + 4 * c);
+      }
+    }
+    float gm = mx;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (s0 + g < ns) gm = fmaxf(gm, m[g].x);
+    const float a = mx == -INFINITY ? 0.f : exp2f(mx - gm);  // rescale of the groups before
+    l *= a;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[j][e] *= a;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float wt = (s0 + g < ns && m[g].x != -INFINITY) ? exp2f(m[g].x - gm) : 0.f;
+      l += m[g].y * wt;
+#pragma unroll
+      for (int j = 0; j < CPT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[j][e] += v[g][j][e] * wt;
+    }
+    mx = gm;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  char* orow = p.o + ((int64_t)(blk.x + row) * p.o_stride + (int64_t)head * p.head_dim) * (p.out_bf16 ? 2 : 4);
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = sub + kMergeTpr * j;
+    if (c < chunks) {
+      if (p.out_bf16) {
+        bf16x4 val;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = (bf16)(acc[j][e] * inv);
+        *reinterpret_cast<bf16x4*>(orow + 8 * c) = val;
+      } else {
+        f32x4 val;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = acc[j][e] * inv;
+        *reinterpret_cast<f32x4*>(orow + 16 * c) = val;
       }
     }
   }
@@ -498,7 +627,7 @@ int validate_desc(const inl_attn_desc* d, int64_t* total_tokens) {
     return fail(INL_E_UNSUPPORTED, "attention: head_dim must be a multiple of 8 in [8, 256]");
   if (d->causal != 0 && d->causal != 1) return fail(INL_E_INVALID, "attention: causal must be 0 or 1");
   if (d->window < -1) return fail(INL_E_INVALID, "attention: window must be -1 or >= 0");
-  if (d->flags & ~INL_ATTN_PV_BF16) return fail(INL_E_INVALID, "attention: unknown flags");
+  if (d->flags & ~(INL_ATTN_PV_BF16 | INL_ATTN_NO_SPLIT)) return fail(INL_E_INVALID, "attention: unknown flags");
   if (!(d->scale > 0.f) || !std::isfinite(d->scale))
     return fail(INL_E_INVALID, "attention: scale must be finite and > 0");
   const int es = dtype_size(d->dtype);
@@ -548,21 +677,47 @@ struct Schedule {
   std::vector<int4> items;
   std::vector<int32_t> unit_hg;   // persistent: head group of each unit
   std::vector<int32_t> wg_start;  // persistent: workgroup b runs units [wg_start[b], wg_start[b + 1])
+  // Generic kernel with a split key range (empty otherwise): partial slot of
+  // each item (-1: writes the output), and per split query block its
+  // {seg_start, seg_len, q0, first slot} and number of parts.
+  std::vector<int32_t> item_part;
+  std::vector<int4> merge_blocks;
+  std::vector<int32_t> merge_parts;
+  int64_t n_slots = 0;            // partial slots (parts), each n_hg * nw * 32 rows
   int block_m = 0;
   int hpw = 1;
   int n_hg = 1;
   KernelCfg cfg{};
 
-  // Device copy, one buffer: items, unit_hg, wg_start (16-byte aligned parts).
+  // Device copy, one buffer: items, unit_hg, wg_start, item_part,
+  // merge_blocks, merge_parts (the uploaded part, 16-byte aligned pieces),
+  // then the partial (max, sum) and O areas, which the kernels fill.
   size_t hg_offset() const { return items.size() * sizeof(int4); }
   size_t wg_offset() const { return hg_offset() + align16(unit_hg.size() * sizeof(int32_t)); }
-  size_t bytes() const { return items.empty() ? 0 : align16(wg_offset() + wg_start.size() * sizeof(int32_t)); }
+  size_t part_offset() const { return wg_offset() + align16(wg_start.size() * sizeof(int32_t)); }
+  size_t mblk_offset() const { return part_offset() + align16(item_part.size() * sizeof(int32_t)); }
+  size_t mparts_offset() const { return mblk_offset() + merge_blocks.size() * sizeof(int4); }
+  size_t upload_bytes() const {
+    return items.empty() ? 0 : align16(mparts_offset() + merge_parts.size() * sizeof(int32_t));
+  }
+  int64_t slot_rows() const { return n_slots * n_hg * cfg.nw * 32; }
+  size_t ml_offset() const { return upload_bytes(); }
+  size_t po_offset() const { return ml_offset() + align16((size_t)slot_rows() * sizeof(float2)); }
+  size_t bytes() const {
+    return n_slots == 0 ? upload_bytes() : po_offset() + (size_t)slot_rows() * cfg.d * sizeof(float);
+  }
   std::vector<char> pack() const {
-    std::vector<char> b(bytes(), 0);
+    std::vector<char> b(upload_bytes(), 0);
     if (b.empty()) return b;
     memcpy(b.data(), items.data(), hg_offset());
     if (!unit_hg.empty()) memcpy(b.data() + hg_offset(), unit_hg.data(), unit_hg.size() * sizeof(int32_t));
     if (!wg_start.empty()) memcpy(b.data() + wg_offset(), wg_start.data(), wg_start.size() * sizeof(int32_t));
+    if (!item_part.empty())
+      memcpy(b.data() + part_offset(), item_part.data(), item_part.size() * sizeof(int32_t));
+    if (!merge_blocks.empty())
+      memcpy(b.data() + mblk_offset(), merge_blocks.data(), merge_blocks.size() * sizeof(int4));
+    if (!merge_parts.empty())
+      memcpy(b.data() + mparts_offset(), merge_parts.data(), merge_parts.size() * sizeof(int32_t));
     return b;
   }
   int64_t n_units() const { return cfg.persistent ? (int64_t)items.size() : (int64_t)items.size() * n_hg; }
@@ -717,7 +872,91 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
   }
 }
 
-int build_schedule(const inl_attn_desc* d, Schedule* s) {
+// Key-range split for the generic f32 kernel. Its workgroups hold one query
+// block each and walk the block's key tiles in order, so a small batch
+// (fewer workgroups than the GPU holds at once) takes as long as its longest
+// block: 4 tiles of about 7 us each for a 256-token causal text at head_dim
+// 128. Cutting blocks into parts of at most `c` tiles, each part a workgroup
+// of its own, and merging the parts afterwards shortens that. `c` minimises
+// an estimate in tile times: the workgroups, longest first, dispatched to
+// the first free slot of the GPU (each costs its tiles plus half a tile of
+// loads and stores), plus one tile for the merge launch if anything is
+// split. Batches with many more workgroups than slots are not split.
+// bf16 descs take the persistent kernels or run unsplit.
+constexpr int kLdsPerCu = 160 * 1024;
+constexpr size_t kMaxPartialBytes = (size_t)256 << 20;
+
+void split_key_ranges(const inl_attn_desc* d, std::vector<CostedItem>& tmp, Schedule* s) {
+  if (d->dtype != INL_F32 || (d->flags & INL_ATTN_NO_SPLIT) || tmp.empty()) return;
+  const int max_tiles = tmp.front().cost;  // sorted longest first
+  if (max_tiles < 2) return;
+  const int64_t resident = (int64_t)device_cus() * std::max(1, kLdsPerCu / std::max(1, s->cfg.lds));
+  if ((int64_t)tmp.size() * s->n_hg > 16 * resident) return;
+  auto est = [&](int c) {
+    std::vector<int> parts;
+    for (const CostedItem& it : tmp)
+      for (int t = 0; t < it.cost; t += c) parts.push_back(std::min(c, it.cost - t));
+    std::stable_sort(parts.begin(), parts.end(), [](int a, int b) { return a > b; });
+    std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
+    for (int64_t i = 0; i < resident; ++i) free_at.push(0.0);
+    double end = 0.0;
+    for (int cost : parts)
+      for (int h = 0; h < s->n_hg; ++h) {
+        const double t = free_at.top() + cost + 0.5;
+        free_at.pop();
+        free_at.push(t);
+        end = std::max(end, t);
+      }
+    return end + (c < max_tiles ? 1.0 : 0.0);
+  };
+  int c_best = max_tiles;
+  double e_best = est(max_tiles);
+  int c = 1;
+  while (2 * c < max_tiles) c *= 2;
+  for (; c >= 1; c /= 2) {
+    const double e = est(c);
+    if (e < e_best - 0.01) { e_best = e; c_best = c; }
+  }
+  if (c_best >= max_tiles) return;
+  int64_t slots = 0;
+  for (const CostedItem& it : tmp)
+    if (it.cost > c_best) slots += (it.cost + c_best - 1) / c_best;
+  const size_t row_bytes = sizeof(float2) + (size_t)s->cfg.d * sizeof(float);
+  if ((size_t)slots * s->n_hg * s->cfg.nw * 32 * row_bytes > kMaxPartialBytes) return;
+  std::vector<CostedItem> out;
+  std::vector<int32_t> part;
+  int32_t next = 0;
+  for (const CostedItem& it : tmp) {
+    if (it.cost <= c_best) {
+      out.push_back(it);
+      part.push_back(-1);
+      continue;
+    }
+    const int lo_t = (int)((uint32_t)it.it.w >> 16), hi_t = it.it.w & 0xffff;
+    s->merge_blocks.push_back(make_int4(it.it.x, it.it.y, it.it.z, next));
+    s->merge_parts.push_back((hi_t - lo_t + c_best - 1) / c_best);
+    for (int t = lo_t; t < hi_t; t += c_best) {
+      const int t1 = std::min(t + c_best, hi_t);
+      out.push_back({make_int4(it.it.x, it.it.y, it.it.z, (t << 16) | t1), t1 - t});
+      part.push_back(next++);
+    }
+  }
+  // longest parts first, as for unsplit items
+  std::vector<size_t> order(out.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return out[a].cost > out[b].cost; });
+  tmp.clear();
+  s->item_part.clear();
+  for (size_t i : order) {
+    tmp.push_back(out[i]);
+    s->item_part.push_back(part[i]);
+  }
+  s->n_slots = next;
+}
+
+// `allow_split`: false for the allocation-free entry, whose static buffer
+// holds schedules, not partial outputs.
+int build_schedule(const inl_attn_desc* d, Schedule* s, bool allow_split = true) {
   int64_t max_t = 0;
   for (int b = 0; b < d->n_texts; ++b)
     max_t = std::max<int64_t>(max_t, d->cu_seqlens_host[b + 1] - d->cu_seqlens_host[b]);
@@ -770,6 +1009,9 @@ int build_schedule(const inl_attn_desc* d, Schedule* s) {
     assign_units(tmp, s->n_hg, s->cfg.head_pairs ? 1 : group / s->hpw, s);
     return INL_OK;
   }
+  if (allow_split) split_key_ranges(d, tmp, s);
+  if ((int64_t)tmp.size() * s->n_hg > INT32_MAX)
+    return fail(INL_E_UNSUPPORTED, "attention: too many tiles for one launch");
   s->items.resize(tmp.size());
   for (size_t i = 0; i < tmp.size(); ++i) s->items[i] = tmp[i].it;
   return INL_OK;
@@ -800,6 +1042,12 @@ AttnParams make_params(const inl_attn_desc* d, const Schedule& s, const void* de
   p.window = d->window;
   p.scale_log2 = d->scale * kLog2e;
   p.out_bf16 = d->out_dtype == INL_BF16;
+  if (s.n_slots) {
+    char* base = (char*)dev_sched;
+    p.item_part = (const int32_t*)(base + s.part_offset());
+    p.part_ml = (float2*)(base + s.ml_offset());
+    p.part_o = (float*)(base + s.po_offset());
+  }
   return p;
 }
 
@@ -826,6 +1074,28 @@ int launch(const Schedule& s, const AttnParams& p, hipStream_t stream) {
   if (blocks > 0x7fffffff) return fail(INL_E_UNSUPPORTED, "attention: too many tiles for one launch");
   hipLaunchKernelGGL(cfg.fn, dim3((unsigned)blocks), dim3(cfg.nw * 64), cfg.lds, stream, p);
   INL_HIP_TRY(hipGetLastError());
+  if (!s.merge_blocks.empty()) {
+    MergeParams m{};
+    const char* base = (const char*)p.items;
+    m.blocks = (const int4*)(base + s.mblk_offset());
+    m.n_parts = (const int32_t*)(base + s.mparts_offset());
+    m.part_o = p.part_o;
+    m.part_ml = p.part_ml;
+    m.o = p.o;
+    m.o_stride = p.o_stride;
+    m.n_hg = p.n_hg;
+    m.nw = cfg.nw;
+    m.rb = p.rb;
+    m.hpw = p.hpw;
+    m.group = p.group;
+    m.groups_per_kv = p.groups_per_kv;
+    m.head_dim = p.head_dim;
+    m.dpad = cfg.d;
+    m.out_bf16 = p.out_bf16;
+    const int64_t mgrid = (int64_t)s.merge_blocks.size() * s.n_hg * cfg.nw * kMergeWgPerWave;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)mgrid), dim3(kMergeThreads), 0, stream, m);
+    INL_HIP_TRY(hipGetLastError());
+  }
   return INL_OK;
 }
 
@@ -890,7 +1160,7 @@ extern "C" int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** p
   if (rc) { delete pl; return rc; }
   const std::vector<char> blob = pl->sched.pack();
   if (!blob.empty()) {
-    hipError_t e = hipMalloc(&pl->d_sched, blob.size());
+    hipError_t e = hipMalloc(&pl->d_sched, pl->sched.bytes());
     if (e != hipSuccess) { delete pl; return hip_fail(e, "hipMalloc(plan)"); }
     e = hipMemcpy(pl->d_sched, blob.data(), blob.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) { (void)hipFree(pl->d_sched); delete pl; return hip_fail(e, "hipMemcpy(plan)"); }
@@ -918,7 +1188,7 @@ extern "C" int inl_attn_plan_create_in(const inl_attn_desc* desc, void* workspac
   if (!rc) rc = ensure_lds_attr(pl->sched.cfg);
   const std::vector<char> blob = rc ? std::vector<char>() : pl->sched.pack();
   if (!rc && !blob.empty()) {
-    if (!workspace || workspace_bytes < blob.size())
+    if (!workspace || workspace_bytes < pl->sched.bytes())
       rc = fail(INL_E_INVALID, "attention: workspace is NULL or smaller than inl_attn_workspace_size()");
     else if (!aligned16(workspace))
       rc = fail(INL_E_INVALID, "attention: workspace must be 16-byte aligned");
@@ -1042,7 +1312,7 @@ extern "C" int inl_attn_varlen_fwd_static(const inl_attn_desc* desc, const void*
   rc = check_ptrs(q, k, v, out, total);
   if (rc) return rc;
   Schedule s;
-  rc = build_schedule(desc, &s);
+  rc = build_schedule(desc, &s, /*allow_split=*/false);
   if (rc) return rc;
   const size_t need = s.bytes();
   if (need == 0) return INL_OK;

@@ -27,6 +27,14 @@ struct AttnParams {
   int32_t window;
   float scale_log2;   // scale * log2(e)
   int32_t out_bf16;
+  // Generic kernel with a split key range (all null otherwise): an item i
+  // with item_part[i] >= 0 covers part of its query block's key tiles and
+  // writes partial slot item_part[i] (per head group and wave: 32 rows of
+  // unnormalised O, row max and row sum) instead of the output;
+  // attn_merge_kernel combines each block's slots into the output.
+  const int32_t* item_part;
+  float* part_o;      // [slot][32 rows][D] f32 (D: the kernel's compiled head dim)
+  float2* part_ml;    // [slot][32 rows] {max (log2 domain, scaled), sum}
 };
 
 constexpr float kLog2e = 1.4426950408889634f;

@@ -64,6 +64,7 @@ class AttnDesc(ctypes.Structure):
 
 
 ATTN_PV_BF16 = 1
+ATTN_NO_SPLIT = 2
 
 
 class NormRopeDesc(ctypes.Structure):

@@ -103,6 +103,15 @@ typedef struct inl_attn_desc {
  * keeps V and P in bf16 (any range, 8x coarser P). */
 #define INL_ATTN_PV_BF16 1
 
+/* f32 descs: a batch too small to fill the GPU (fewer query blocks x head
+ * groups than workgroups the GPU holds at once) has its longer query blocks'
+ * key ranges split into parts that run as separate workgroups, and a second
+ * kernel merges the parts' partial outputs (max, sum and unnormalised O,
+ * kept in the plan's device memory). Results then differ from the unsplit
+ * order of summation by f32 rounding only. This flag keeps every block in
+ * one workgroup (one launch, no partials). bf16 descs are never split. */
+#define INL_ATTN_NO_SPLIT 2
+
 /* An attention plan: the packed texts' tile schedule, resident on the
  * device. Build it once per batch and reuse it for every layer of that
  * batch that has the same desc fields (all layers of one kind). */
@@ -144,7 +153,8 @@ int inl_attn_varlen_fwd(const inl_attn_desc* desc, const void* q,
 /* Allocation-free one-shot form. It has no counterpart in the reference: it
  * is for callers that cannot allocate device memory per call (tight serving
  * loops, harnesses that forbid hipMalloc). It runs the same kernels as
- * inl_attn_varlen_fwd, with the same results, but keeps the schedule in a
+ * inl_attn_varlen_fwd with INL_ATTN_NO_SPLIT set (the same results for
+ * every bf16 desc; f32 batches are not split), but keeps the schedule in a
  * static device buffer of the library, INL_ATTN_STATIC_SCHEDULE_BYTES per
  * GPU (held by each GPU the library runs on until the process ends), so it
  * takes no workspace and calls no allocator. A batch whose schedule is

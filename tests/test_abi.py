@@ -198,3 +198,26 @@ def test_asm_load_kernels_use_no_scratch():
                  if re.search(r'asm volatile\("buffer_load', p.read_text())
                  or re.search(r'vmcnt\(%', p.read_text()) or '"attn_stream.hpp"' in p.read_text()}
     assert asm_loads <= b.NO_SCRATCH, asm_loads - b.NO_SCRATCH
+
+
+def test_small_f32_batches_split_their_key_ranges():
+    """f32 batches too small to fill the GPU get a key-range split (partial
+    outputs in the plan's memory, so a larger workspace); bf16 descs, large
+    batches and INL_ATTN_NO_SPLIT do not."""
+    import inl_hip
+    n = ctypes.c_size_t()
+
+    def ws(cu, dtype, flags=0):
+        d = inl_hip.make_attn_desc(cu, 16, 8, 128, causal=True, dtype=dtype, flags=flags)
+        assert inl_hip._ws_size(ctypes.byref(d), ctypes.byref(n)) == 0, inl_hip.last_error()
+        return n.value
+
+    small = [0, 16, 116, 372, 409, 609, 738, 802, 1052]   # configuration 1's size: 8 texts
+    one_slot_group = 8 * 4 * 32 * (8 + 128 * 4)           # head groups x waves x rows x (max, sum, O)
+    assert ws(small, "f32") >= ws(small, "f32", inl_hip.ATTN_NO_SPLIT) + one_slot_group
+    assert ws(small, "bf16") == ws(small, "bf16", inl_hip.ATTN_NO_SPLIT)
+    big = list(range(0, 64 * 2048 + 1, 2048))              # 64 texts x 2048 fill the GPU
+    assert ws(big, "f32") == ws(big, "f32", inl_hip.ATTN_NO_SPLIT)
+    bad = inl_hip.make_attn_desc(small, 16, 8, 128, causal=True, dtype="f32", flags=4)
+    assert inl_hip._ws_size(ctypes.byref(bad), ctypes.byref(n)) != 0
+    assert "unknown flags" in inl_hip.last_error()

@@ -108,6 +108,45 @@ def test_f32_matches_oracle(case, cuda, inl):
     assert err <= 1e-5, f"{name}: f32 max abs err {err:.3g}"
 
 
+SPLIT_CASES = [
+    # f32 batches small enough that the plan splits their longer query
+    # blocks' key ranges over several workgroups and merges the parts.
+    ("config1_like", [16, 100, 256, 37, 200, 129, 64, 250], 16, 8, 128, True, -1, 128 ** -0.5),
+    ("one_long_causal", [1024], 16, 8, 128, True, -1, 128 ** -0.5),
+    ("window_d64", [1500, 3], 12, 12, 64, False, 64, 64 ** -0.5),
+    ("d256_causal_gqa8", [700, 5], 16, 2, 256, True, -1, 256 ** -0.5),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_f32_split_key_ranges(case, cuda, inl):
+    """The split plan launches more work items than the unsplit one; both
+    match the oracle within 1e-5 (f32 output) and within 1e-5 plus half a
+    bf16 ulp (bf16 output of f32 inputs)."""
+    import torch
+    name, lengths, hq, hkv, d, causal, window, scale = case
+    (q, k, v), (qh, kh, vh) = _inputs(lengths, hq, hkv, d, 5, torch.float32, torch, cuda, scale)
+    cu = oa.cu_from_lengths(lengths)
+    mk = lambda flags: inl.make_attn_desc(cu.tolist(), hq, hkv, d, causal=causal, window=window, scale=scale,
+                                          dtype="f32", out_dtype="f32", flags=flags)
+    split, whole = inl.AttnPlan(mk(0)), inl.AttnPlan(mk(inl.ATTN_NO_SPLIT))
+    assert split.info()["tiles"] > whole.info()["tiles"], (split.info(), whole.info())
+    split.close()
+    whole.close()
+    ref = oa.varlen_attention(qh, kh, vh, cu, causal=causal, window=window, scale=scale)
+    print(f"case={name} f32 split", flush=True)
+    for flags in (0, inl.ATTN_NO_SPLIT):
+        out = inl.varlen_attention(q, k, v, cu.tolist(), causal=causal, window=window, scale=scale, flags=flags)
+        torch.cuda.synchronize()
+        err = np.abs(out.cpu().numpy().astype(np.float64) - ref).max()
+        assert err <= 1e-5, f"{name} flags={flags}: f32 max abs err {err:.3g}"
+    out16 = inl.varlen_attention(q, k, v, cu.tolist(), causal=causal, window=window, scale=scale,
+                                 out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    got = out16.float().cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-5 + _half_ulp_bf16(ref)), f"{name}: bf16 output of the merge"
+
+
 def test_plan_reuse_and_empty_texts(cuda, inl):
     """A plan is reusable across calls; zero-length texts own no rows."""
     import torch
