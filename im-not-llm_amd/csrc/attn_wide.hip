@@ -11,10 +11,12 @@
 //   - A workgroup is 4 waves, one per SIMD, on one CU, walking the same
 //     host-built stream of work units as attn_pp.hip. Each wave owns 32
 //     query rows of one head; a unit is hpw heads x 4 / hpw blocks of rows.
-//   - Tiles are 32 keys. Iteration j runs the softmax of tile j in the
-//     shadow of S^T = K Q^T of tile j + 1 (S^T double-buffered), then
-//     O^T += V_j^T P_j^T in the shadow of the bf16 -> fp16 conversion of the
-//     wave's slice of V_{j+1} and the loads of tile j + 3.
+//   - Tiles are 32 keys. Iteration j computes P of tile j's first 16 keys
+//     in the shadow of S^T = K Q^T of tile j + 1 (S^T double-buffered), P of
+//     its other 16 keys beside O^T += V^T P^T of the first 16, and the
+//     bf16 -> fp16 conversion of the wave's slice of V_{j+1} beside the PV
+//     of the second 16; then it issues the loads of tile j + 3. The row sum
+//     of P is one more MFMA per 16 keys, with an all-ones A operand.
 //   - 4 LDS stages of K (bf16) and V (fp16 after conversion), 16 KiB each;
 //     one barrier per tile.
 //
@@ -243,7 +245,7 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[i][r] = 0.f;
   float m_i = -INFINITY;
-  float l_i = 0.f;   // row sum of the rounded fp16 P (per lane half)
+  float l_i = 0.f;   // row sum of the rounded fp16 P (whole row in every lane)
   f32x16 sacc[2];    // S^T of tiles j (sacc[j & 1]) and j + 1
   u32x4 pk[PKS];     // P^T operand per PV k-step
   const float c2 = p.scale_log2;
@@ -333,7 +335,7 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
   // that each store writes 8 whole 128-byte lines. `stg`: 4 KB of LDS that
   // no other wave touches during this step.
   auto store_out = [&](uint32_t stg) __attribute__((always_inline)) {
-    const float l_tot = half_sum(l_i);
+    const float l_tot = l_i;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (p.out_bf16) {
       const uint32_t wr = stg + lq * 128;
@@ -448,18 +450,29 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
           oacc[i][r] = y;
         }
     }
-    // P of tile j beside QK^T of tile j + 1; the fragment reads of that
-    // QK^T and of tile j's PV (its V was converted last iteration) go out
-    // here too, ahead of their MFMAs.
+    // Three MFMA groups, each with VALU and LDS work in its shadow:
+    //   QK^T of tile j + 1 (16)   P of k-step 0, its V fragments, K reads
+    //   PV k-step 0 (8 + 1)       P of k-step 1, its V fragments
+    //   PV k-step 1 (8 + 1)       conversion of tile j + 1's V
+    // The row sum of P comes from the matrix core: one extra MFMA per k-step
+    // with an all-ones A operand sums the rounded fp16 P over the k-step's
+    // keys into every row of its accumulator (f32 accumulation).
     const float base = m_i == -INFINITY ? 0.f : m_i;
     u32x4 kr[KST];
 #pragma unroll
     for (int st = 0; st < KST; ++st) kr[st] = kfrag(st_nxt, st);
-    f16x8 vf[PKS][NDB];
+    f16x8 vf0[NDB], vf1[NDB];
 #pragma unroll
-    for (int ks = 0; ks < PKS; ++ks)
+    for (int db = 0; db < NDB; ++db) vf0[db] = vfrag(st_cur, 0, db);
+    auto make_pk = [&](int ks) __attribute__((always_inline)) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) vf[ks][db] = vfrag(st_cur, ks, db);
+      for (int e = 0; e < 8; e += 2) {
+        f32x2 pr = {__builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[8 * ks + e], c2, -base)),
+                    __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[8 * ks + e + 1], c2, -base))};
+        pk[ks][e / 2] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pr, f16x2));
+      }
+    };
+    make_pk(0);
     {
       const f32x16 zero = {};
 #pragma unroll
@@ -468,48 +481,58 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
                                                         __builtin_bit_cast(bf16x8, qreg[st]),
                                                         st == 0 ? zero : s_nxt, 0, 0, 0);
     }
-    float lt0 = 0.f, lt1 = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < PKS; ++ks) {
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        f32x2 pr = {__builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[8 * ks + e], c2, -base)),
-                    __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[8 * ks + e + 1], c2, -base))};
-        const uint32_t pair = __builtin_bit_cast(uint32_t, __builtin_convertvector(pr, f16x2));
-        pk[ks][e / 2] = pair;
-        asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(lt0) : "v"(pair));
-        asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lt1) : "v"(pair));
-      }
-    }
-    l_i += lt0 + lt1;
-    // 8 reads ahead, then per QK^T MFMA: four VALU and two more reads
+    // 8 K reads ahead; per QK^T MFMA one more K read, one V read (8 of 16)
+    // and the VALU of P's first k-step
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
     for (int i = 0; i < KST; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // the next unit's Q, once the last QK^T of the current one is issued
-    if (__builtin_expect(qt + 1 == qhi && qu + 1 < nu, 0)) load_q_of(qu + 1);
-
-    // PV of tile j beside the conversion of tile j + 1 and the loads of tile j + 3
+    const f16x8 ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
+                        (_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+    f32x16 lsum;
+    make_pk(1);
 #pragma unroll
-    for (int ks = 0; ks < PKS; ++ks)
+    for (int db = 0; db < NDB; ++db) vf1[db] = vfrag(st_cur, 1, db);
+    {
+      const f32x16 zero = {};
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[ks][db], __builtin_bit_cast(f16x8, pk[ks]), oacc[db], 0, 0, 0);
-    conv(st_nxt);
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf0[db], __builtin_bit_cast(f16x8, pk[0]), oacc[db], 0, 0, 0);
+      lsum = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, __builtin_bit_cast(f16x8, pk[0]), zero, 0, 0, 0);
+    }
 #pragma unroll
-    for (int i = 0; i < DMA_PARTS; ++i) dma_part(i, st_dma);
-#pragma unroll
-    for (int i = 0; i < PKS * NDB; ++i) {
+    for (int i = 0; i < NDB + 1; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf1[db], __builtin_bit_cast(f16x8, pk[1]), oacc[db], 0, 0, 0);
+    lsum = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, __builtin_bit_cast(f16x8, pk[1]), lsum, 0, 0, 0);
+    conv(st_nxt);
+#pragma unroll
+    for (int i = 0; i < NDB + 1; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // The next unit's Q once the current one's last QK^T has run (its wait
+    // retires the loads issued before it, not this step's), then the loads
+    // of tile j + 3: issued at the end of the step, they run faster than
+    // anywhere earlier, where they share LDS with the fragment reads.
+    if (__builtin_expect(qt + 1 == qhi && qu + 1 < nu, 0)) load_q_of(qu + 1);
+#pragma unroll
+    for (int i = 0; i < DMA_PARTS; ++i) dma_part(i, st_dma);
+    __builtin_amdgcn_sched_barrier(0);
+    l_i += lsum[0];
     dma_advance();
     // the QK cursor moves to tile j + 2
     if (__builtin_expect(++qt == qhi, 0) && ++qu < nu) {
