@@ -9,6 +9,7 @@
 // pointers allow it (one lane per 8 bf16 or 4 f32 values).
 
 #include <cmath>
+#include <type_traits>
 
 #include "inl_common.hpp"
 
@@ -42,14 +43,60 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const ch
     o[i] = ok ? ldf<T>(row + i * (int)sizeof(T)) : __builtin_nanf("");
 }
 
+// Sum of x over the 64 lanes of the wave, in every lane: DPP within each
+// row of 16 lanes (pairs, quads, mirrored halves, mirrored rows), then
+// v_permlane16_swap and v_permlane32_swap across the rows.
+__device__ __forceinline__ float wave_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  x = a + b;
+  a = x;
+  b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+
+// 4 consecutive values at byte address p of a T array, as f32. VEC: one
+// vector access (p aligned to 4 * sizeof(T)); otherwise four scalar ones.
+template <typename T, bool VEC>
+__device__ __forceinline__ f32x4 ld4(const char* p) {
+  if constexpr (VEC && sizeof(T) == 2) {
+    const u32x2 b = *reinterpret_cast<const u32x2*>(p);
+    return (f32x4){__builtin_bit_cast(float, b[0] << 16), __builtin_bit_cast(float, b[0] & 0xffff0000u),
+                   __builtin_bit_cast(float, b[1] << 16), __builtin_bit_cast(float, b[1] & 0xffff0000u)};
+  } else if constexpr (VEC) {
+    return *reinterpret_cast<const f32x4*>(p);
+  } else {
+    return (f32x4){ldf<T>(p), ldf<T>(p + sizeof(T)), ldf<T>(p + 2 * sizeof(T)), ldf<T>(p + 3 * sizeof(T))};
+  }
+}
+template <typename T, bool VEC>
+__device__ __forceinline__ void st4(char* p, const f32x4& v) {
+  if constexpr (VEC && sizeof(T) == 2) {
+    const bf16x2 lo = __builtin_convertvector((f32x2){v[0], v[1]}, bf16x2);
+    const bf16x2 hi = __builtin_convertvector((f32x2){v[2], v[3]}, bf16x2);
+    *reinterpret_cast<u32x2*>(p) = (u32x2){__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+  } else if constexpr (VEC) {
+    *reinterpret_cast<f32x4*>(p) = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) stf<T>(p + e * sizeof(T), v[e]);
+  }
+}
+
 // ---- RMSNorm of f32 rows into TO: one wave per row ----
 // y = x / sqrt(mean(x^2) + eps) * w (w in TW, the model dtype). Each lane
-// sums its 4-float chunks of the row; 64-lane xor-shuffle reduction. With
-// K > 0 the row (at most K * 256 values) stays in registers between the two
-// passes: K loads per lane issued at once from clamped addresses (masked
-// after, so no load waits behind a branch), the row read once. K = 0 reads
-// a longer row twice.
-template <typename TW, typename TO, int K>
+// holds 4-value chunks of the row; the sum of squares is a wave_sum. With
+// K > 0 the row (at most K * 256 values) and its weights stay in registers
+// between the two passes: every load is issued first, at a clamped address
+// (masked after, so no load waits behind a branch). K = 0 reads a longer row
+// twice. VEC: the weights and the output are read and written 4 values at a
+// time (the host checks their alignment).
+template <typename TW, typename TO, int K, bool VEC>
 __global__ __launch_bounds__(256) void rms_rows_kernel(const float* x, int64_t xs, int64_t rows, int32_t dim,
                                                        const char* w, float eps, char* y, int64_t ys) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -57,41 +104,38 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(const float* x, int64_t x
   if (r >= rows) return;
   const float* xr = x + r * xs;
   char* yr = y + r * ys * (int64_t)sizeof(TO);
-  auto put = [&](int i, const f32x4& v, float inv) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float wv = w ? ldf<TW>(w + (i + e) * (int)sizeof(TW)) : 1.f;
-      stf<TO>(yr + (i + e) * (int)sizeof(TO), v[e] * inv * wv);
-    }
-  };
+  const f32x4 one = {1.f, 1.f, 1.f, 1.f};
   float ss = 0.f;
   if constexpr (K > 0) {
-    f32x4 held[K];
+    f32x4 held[K], wv[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int i = lane * 4 + 256 * k;
-      held[k] = *reinterpret_cast<const f32x4*>(xr + (i < dim ? i : dim - 4));
+      const int ic = i < dim ? i : dim - 4;
+      held[k] = *reinterpret_cast<const f32x4*>(xr + ic);
+      wv[k] = w ? ld4<TW, VEC>(w + ic * (int)sizeof(TW)) : one;
     }
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       if (lane * 4 + 256 * k >= dim) held[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
       ss += (held[k][0] * held[k][0] + held[k][1] * held[k][1]) + (held[k][2] * held[k][2] + held[k][3] * held[k][3]);
     }
-    for (int m = 32; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
-    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)dim + eps);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int i = lane * 4 + 256 * k;
-      if (i < dim) put(i, held[k], inv);
+      if (i < dim) st4<TO, VEC>(yr + i * (int)sizeof(TO), held[k] * inv * wv[k]);
     }
   } else {
     for (int i = lane * 4; i < dim; i += 256) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(xr + i);
       ss += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
     }
-    for (int m = 32; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
-    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
-    for (int i = lane * 4; i < dim; i += 256) put(i, *reinterpret_cast<const f32x4*>(xr + i), inv);
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)dim + eps);
+    for (int i = lane * 4; i < dim; i += 256) {
+      const f32x4 wq = w ? ld4<TW, VEC>(w + i * (int)sizeof(TW)) : one;
+      st4<TO, VEC>(yr + i * (int)sizeof(TO), *reinterpret_cast<const f32x4*>(xr + i) * inv * wq);
+    }
   }
 }
 
@@ -183,21 +227,30 @@ extern "C" int inl_rms_norm_rows_fwd(int64_t rows, int32_t dim, const float* x, 
   // chunks of 256 values a lane holds: the smallest of 1, 2, 4, 8 that covers
   // the row, 0 (two passes) beyond 2048
   const int K = dim <= 256 ? 1 : dim <= 512 ? 2 : dim <= 1024 ? 4 : dim <= 2048 ? 8 : 0;
-  auto launch = [&](auto tw, auto to) {
+  // Vector weight and output accesses when every 4-value group is aligned
+  // to 4 elements: the pointers and the output row stride.
+  const int wsz = dtype_size(weight_dtype), osz = dtype_size(out_dtype);
+  const bool vec = ((uintptr_t)w % (4 * wsz)) == 0 && ((uintptr_t)y % (4 * osz)) == 0 && ys % 4 == 0;
+  auto launch = [&](auto tw, auto to, auto vtag) {
     using TW = decltype(tw);
     using TO = decltype(to);
+    constexpr bool V = decltype(vtag)::value;
     switch (K) {
-      case 1: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 1>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
-      case 2: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 2>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
-      case 4: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 4>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
-      case 8: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 8>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
-      default: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 0>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys);
+      case 1: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 1, V>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
+      case 2: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 2, V>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
+      case 4: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 4, V>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
+      case 8: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 8, V>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys); break;
+      default: hipLaunchKernelGGL((rms_rows_kernel<TW, TO, 0, V>), grid, dim3(256), 0, st, x, xs, rows, dim, w, eps, (char*)y, ys);
     }
   };
-  if (weight_dtype == INL_BF16 && out_dtype == INL_BF16) launch(bf16{}, bf16{});
-  else if (weight_dtype == INL_BF16) launch(bf16{}, float{});
-  else if (out_dtype == INL_BF16) launch(float{}, bf16{});
-  else launch(float{}, float{});
+  auto launch_v = [&](auto tw, auto to) {
+    if (vec) launch(tw, to, std::true_type{});
+    else launch(tw, to, std::false_type{});
+  };
+  if (weight_dtype == INL_BF16 && out_dtype == INL_BF16) launch_v(bf16{}, bf16{});
+  else if (weight_dtype == INL_BF16) launch_v(bf16{}, float{});
+  else if (out_dtype == INL_BF16) launch_v(float{}, bf16{});
+  else launch_v(float{}, float{});
   INL_HIP_TRY(hipGetLastError());
   return INL_OK;
 }

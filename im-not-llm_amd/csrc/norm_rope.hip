@@ -77,6 +77,81 @@ __device__ __forceinline__ void store8(char* p, const float (&v)[8]) {
   }
 }
 
+// Cross-lane helpers on the VALU (DPP and v_permlane*_swap), in place of
+// LDS-routed shuffles. dpp(x, ctrl): lane i reads the lane that `ctrl`
+// names within its row of 16.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// out[e] = in[e] of lane (lane ^ m), for m a power of two below 64
+// (uniform): one switch for the 8 values. Called with every lane of the
+// wave active (a DPP read of a lane outside exec returns 0).
+__device__ __forceinline__ void xor_lanes8(const float (&in)[8], float (&out)[8], int m, int lane) {
+  switch (m) {
+    case 1:
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = dpp<0xB1>(in[e]);      // quad_perm [1, 0, 3, 2]
+      break;
+    case 2:
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = dpp<0x4E>(in[e]);      // quad_perm [2, 3, 0, 1]
+      break;
+    case 4: {
+      const bool hi = lane & 4;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float down = dpp<0x114>(in[e]);   // row_shr:4: lane i - 4
+        const float up = dpp<0x104>(in[e]);     // row_shl:4: lane i + 4
+        out[e] = hi ? down : up;
+      }
+      break;
+    }
+    case 8:
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = dpp<0x128>(in[e]);     // row_ror:8
+      break;
+    case 16: {
+      const bool odd = lane & 16;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = in[e], b = in[e];   // a: rows (0, 0, 2, 2), b: rows (1, 1, 3, 3)
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        out[e] = odd ? a : b;
+      }
+      break;
+    }
+    default: {
+      const bool upper = lane & 32;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = in[e], b = in[e];   // a: halves (0, 0), b: halves (1, 1)
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        out[e] = upper ? a : b;
+      }
+    }
+  }
+}
+// Sum of x over each aligned group of G lanes, in every lane of the group.
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (G >= 2) x += dpp<0xB1>(x);
+  if constexpr (G >= 4) x += dpp<0x4E>(x);
+  if constexpr (G >= 8) x += dpp<0x141>(x);    // row_half_mirror: quad q <-> quad 1 - q of each 8
+  if constexpr (G >= 16) x += dpp<0x140>(x);   // row_mirror: 8-lane halves of each row
+  if constexpr (G >= 32) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    x = a + b;
+  }
+  if constexpr (G >= 64) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    x = a + b;
+  }
+  return x;
+}
+
 // A group of G = head_dim / 8 lanes owns one token: each lane holds 8
 // elements of a head row. The token's norm weight, table row and the lane's
 // cos/sin columns are loaded once per group of HB = 4 heads of the token
@@ -84,10 +159,10 @@ __device__ __forceinline__ void store8(char* p, const float (&v)[8]) {
 // read and y written and the tables cost a quarter of that in cache reads;
 // the 4 loads of a lane go out together. Every lane of a wave runs the head
 // step the same number of times (the shuffles need all of them).
-template <typename TI, typename TO>
+template <typename TI, typename TO, int G>
 __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
   constexpr int HB = 4;                          // heads per step
-  const int G = p.head_dim >> 3;                 // lanes per row (power of two <= 64)
+  // G = head_dim / 8 lanes per row (a power of two <= 64)
   const int lane = threadIdx.x & 63;
   const int j = lane & (G - 1);                  // chunk of the row this lane owns
   // lane group -> (token, chunk of HB heads)
@@ -126,6 +201,11 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
   for (int e = 0; e < 8; ++e) { c[e] = 1.f; sn[e] = 0.f; }
   bool bad_pos = false;
   int sec_lanes = 0, sec0 = 0;
+  // Partner distance of the half-split lanes. A power of two puts every
+  // partner at lane ^ half_lanes (sections start at multiples of sec_lanes),
+  // so the exchange runs on DPP / permlane instead of an LDS shuffle.
+  int half_lanes = 0;
+  bool xor_partner = false;
   if (p.rotary_dim == 8 && p.sections == 1) {
     mode = j == 0 ? 1 : 0;
   } else if (p.rotary_dim > 0) {
@@ -136,7 +216,8 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
       sec_lanes = p.rotary_dim >> 3;
       sec0 = 0;
     }
-    const int half_lanes = sec_lanes >> 1;
+    half_lanes = sec_lanes >> 1;
+    xor_partner = half_lanes > 0 && (half_lanes & (half_lanes - 1)) == 0;
     const int jj = j - sec0;                         // chunk inside the section
     if (jj >= 0 && jj < sec_lanes) {
       mode = 2;
@@ -187,7 +268,7 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
-        for (int m = G >> 1; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        ss = group_sum<G>(ss);
         const float inv = 1.0f / sqrtf(ss / (float)p.head_dim + p.eps);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -205,8 +286,11 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
       }
       if (p.rotary_dim > 0 && !(p.rotary_dim == 8 && p.sections == 1)) {
         float pv[8];
+        if (xor_partner)
+          xor_lanes8(v[i], pv, half_lanes, lane);
+        else
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = __shfl(v[i][e], partner, 64);
+          for (int e = 0; e < 8; ++e) pv[e] = __shfl(v[i][e], partner, 64);
         if (mode == 2)
 #pragma unroll
           for (int e = 0; e < 8; ++e)
@@ -291,14 +375,24 @@ extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, voi
     return fail(INL_E_UNSUPPORTED, "norm_rope: tokens x head chunks must stay below 2^31");
   const int64_t blocks = (groups + groups_per_block - 1) / groups_per_block;
   hipStream_t st = (hipStream_t)stream;
-  if (d->dtype == INL_BF16 && d->out_dtype == INL_BF16)
-    hipLaunchKernelGGL((norm_rope_kernel<bf16, bf16>), dim3((unsigned)blocks), dim3(256), 0, st, p);
-  else if (d->dtype == INL_BF16)
-    hipLaunchKernelGGL((norm_rope_kernel<bf16, float>), dim3((unsigned)blocks), dim3(256), 0, st, p);
-  else if (d->out_dtype == INL_BF16)
-    hipLaunchKernelGGL((norm_rope_kernel<float, bf16>), dim3((unsigned)blocks), dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL((norm_rope_kernel<float, float>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  auto launch = [&](auto ti, auto to) {
+    using TI = decltype(ti);
+    using TO = decltype(to);
+    const dim3 grid((unsigned)blocks), block(256);
+    switch (G) {
+      case 1: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 1>), grid, block, 0, st, p); break;
+      case 2: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 2>), grid, block, 0, st, p); break;
+      case 4: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 4>), grid, block, 0, st, p); break;
+      case 8: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 8>), grid, block, 0, st, p); break;
+      case 16: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 16>), grid, block, 0, st, p); break;
+      case 32: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 32>), grid, block, 0, st, p); break;
+      default: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 64>), grid, block, 0, st, p);
+    }
+  };
+  if (d->dtype == INL_BF16 && d->out_dtype == INL_BF16) launch(bf16{}, bf16{});
+  else if (d->dtype == INL_BF16) launch(bf16{}, float{});
+  else if (d->out_dtype == INL_BF16) launch(float{}, bf16{});
+  else launch(float{}, float{});
   INL_HIP_TRY(hipGetLastError());
   return INL_OK;
 }

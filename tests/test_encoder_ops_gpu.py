@@ -97,3 +97,38 @@ def test_embed_rms_swiglu(dtype, cuda, inl):
         assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
     else:
         assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-5)
+
+
+@pytest.mark.parametrize("dim", [256, 1000, 1024, 3000])
+def test_rms_rows_vector_and_scalar_paths(dim, cuda, inl):
+    """RMSNorm rows at every register layout (one chunk, a partial last
+    chunk, four chunks, two passes), with no weight, an aligned weight (the
+    4-value vector path) and a weight and output one element off alignment
+    (the scalar path), in f32 and bf16."""
+    import torch
+    n = 37
+    x = _rand(torch, cuda, (n, dim), 11)
+    x64 = x.cpu().numpy().astype(np.float64)
+    for td in (torch.float32, torch.bfloat16):
+        big = (1 + 0.2 * _rand(torch, cuda, (dim + 8,), 12)).to(td)
+        for wname, w in (("none", None), ("aligned", big[:dim]), ("offset", big[1:1 + dim])):
+            w64 = np.ones(dim) if w is None else w.float().cpu().numpy().astype(np.float64)
+            ref = op.rms_norm(x64, w64, 1e-6)
+            outs = {"contiguous": inl.rms_norm_rows(x, w, eps=1e-6, out_dtype=td)}
+            buf = torch.full((n, dim + 8), float("nan"), dtype=td, device=cuda)
+            view = buf[:, 1:1 + dim]
+            wdt = inl.INL_F32 if w is None else inl._dtype_code(w.dtype)
+            rc = inl._rms_rows(n, dim, x.data_ptr(), x.stride(0), None if w is None else w.data_ptr(), wdt, 1e-6,
+                               inl._dtype_code(td), view.data_ptr(), buf.stride(0), None)
+            assert rc == 0, inl.last_error()
+            outs["offset"] = view
+            torch.cuda.synchronize()
+            print(f"case=rms_rows dim={dim} {td} weight={wname}", flush=True)
+            for oname, y in outs.items():
+                got = y.float().cpu().numpy()
+                if td == torch.float32:
+                    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max(), (wname, oname)
+                else:
+                    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6), (wname, oname)
+            # the padding around the offset view is untouched
+            assert torch.isnan(buf[:, 0]).all() and torch.isnan(buf[:, 1 + dim:]).all()

@@ -79,6 +79,10 @@ CASES = [
     ("tiny_head_dim16", 4, 16, True, True, 1e4, 16, 0),
     ("tiny_head_dim8", 4, 8, False, False, 1e4, 8, 0),
     ("partial_rotary8", 4, 32, True, True, 1e4, 8, 0),
+    # partner lanes 32 apart (v_permlane32_swap) and a 64-lane norm sum
+    ("wide_head_dim512", 2, 512, True, True, 1e4, 512, 0),
+    # partner lanes 3 apart: not a power of two, the shuffle path
+    ("partial_rotary48", 4, 64, True, True, 1e4, 48, 0),
 ]
 
 
