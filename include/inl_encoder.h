@@ -34,7 +34,11 @@ extern "C" {
  * Strides are elements between rows (0 = packed). `workspace` (device, may be
  * NULL with 0 bytes) lets hipBLASLt pick kernels that need scratch; size it
  * with inl_linear_workspace_size. Runs hipBLASLt; per device and shape the
- * first call queries its heuristic, later calls reuse the choice. */
+ * first call queries its heuristic and, unless `stream` is capturing a
+ * graph, times up to 16 of its candidates on the call's operands (into a
+ * scratch output it allocates and frees; y is not touched) and keeps the
+ * fastest. That first call synchronises the stream; later calls reuse the
+ * choice and allocate nothing. */
 int inl_linear_workspace_size(size_t* bytes);
 int inl_linear_fwd(int64_t m, int64_t n, int64_t k, int32_t in_dtype,
                    const void* x, int64_t x_stride, const void* w,
