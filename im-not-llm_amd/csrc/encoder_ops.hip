@@ -12,6 +12,7 @@
 #include <type_traits>
 
 #include "inl_common.hpp"
+#include "lanes.hpp"
 
 namespace inl {
 
@@ -41,23 +42,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const ch
   float* o = out + t * out_stride;
   for (int i = threadIdx.x; i < hidden; i += blockDim.x)
     o[i] = ok ? ldf<T>(row + i * (int)sizeof(T)) : __builtin_nanf("");
-}
-
-// Sum of x over the 64 lanes of the wave, in every lane: DPP within each
-// row of 16 lanes (pairs, quads, mirrored halves, mirrored rows), then
-// v_permlane16_swap and v_permlane32_swap across the rows.
-__device__ __forceinline__ float wave_sum(float x) {
-  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
-  float a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  x = a + b;
-  a = x;
-  b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return a + b;
 }
 
 // 4 consecutive values at byte address p of a T array, as f32. VEC: one

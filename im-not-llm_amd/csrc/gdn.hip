@@ -21,6 +21,7 @@
 #include "../../include/inl_gdn.h"
 #include "attn_kernels.hpp"
 #include "inl_common.hpp"
+#include "lanes.hpp"
 
 #pragma clang fp contract(off)
 
@@ -303,11 +304,8 @@ __global__ __launch_bounds__(GDN_WAVES * 64) void gdn_rule_kernel(GdnRuleParams 
       const int i = w + GDN_WAVES * u;
       float sq = rq[u][0] * rq[u][0] + rq[u][1] * rq[u][1];
       float sk = rk[u][0] * rk[u][0] + rk[u][1] * rk[u][1];
-#pragma unroll
-      for (int m = 32; m > 0; m >>= 1) {
-        sq += __shfl_xor(sq, m, 64);
-        sk += __shfl_xor(sk, m, 64);
-      }
+      sq = wave_sum(sq);
+      sk = wave_sum(sk);
       const float qn = __fsqrt_rn(sq + 1e-6f), kn = __fsqrt_rn(sk + 1e-6f);
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
@@ -365,7 +363,7 @@ __global__ __launch_bounds__(GDN_WAVES * 64) void gdn_rule_kernel(GdnRuleParams 
       m3 = __builtin_fmaf(Sp[j + 3], kc[j + 3], m3);
     }
     const float mem = D * quad_sum((m0 + m1) + (m2 + m3));
-    const float u = (v - mem) * bet / D;
+    const float u = (v - mem) * bet * __builtin_amdgcn_rcpf(D);
 #pragma unroll
     for (int j = 0; j < GDN_ROWS; ++j) Sp[j] = __builtin_fmaf(kc[j], u, Sp[j]);
     float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "inl_common.hpp"
+#include "lanes.hpp"
 
 namespace inl {
 
@@ -77,13 +78,6 @@ __device__ __forceinline__ void store8(char* p, const float (&v)[8]) {
   }
 }
 
-// Cross-lane helpers on the VALU (DPP and v_permlane*_swap), in place of
-// LDS-routed shuffles. dpp(x, ctrl): lane i reads the lane that `ctrl`
-// names within its row of 16.
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
-}
 // out[e] = in[e] of lane (lane ^ m), for m a power of two below 64
 // (uniform): one switch for the 8 values. Called with every lane of the
 // wave active (a DPP read of a lane outside exec returns 0).
@@ -132,26 +126,6 @@ __device__ __forceinline__ void xor_lanes8(const float (&in)[8], float (&out)[8]
     }
   }
 }
-// Sum of x over each aligned group of G lanes, in every lane of the group.
-template <int G>
-__device__ __forceinline__ float group_sum(float x) {
-  if constexpr (G >= 2) x += dpp<0xB1>(x);
-  if constexpr (G >= 4) x += dpp<0x4E>(x);
-  if constexpr (G >= 8) x += dpp<0x141>(x);    // row_half_mirror: quad q <-> quad 1 - q of each 8
-  if constexpr (G >= 16) x += dpp<0x140>(x);   // row_mirror: 8-lane halves of each row
-  if constexpr (G >= 32) {
-    float a = x, b = x;
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    x = a + b;
-  }
-  if constexpr (G >= 64) {
-    float a = x, b = x;
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    x = a + b;
-  }
-  return x;
-}
-
 // A group of G = head_dim / 8 lanes owns one token: each lane holds 8
 // elements of a head row. The token's norm weight, table row and the lane's
 // cos/sin columns are loaded once per group of HB = 4 heads of the token
