@@ -450,8 +450,7 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const TC* __restric
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 4; ++e) ss += val[e] * val[e];
-#pragma unroll
-  for (int m = 16; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 32);
+  ss = group_sum<32>(ss);
   const float inv_dv = __fdiv_rn(1.0f, (float)dv);
   const float scale = __fsqrt_rn(ss * inv_dv + eps);
   if (!live) return;

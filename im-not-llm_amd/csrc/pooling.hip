@@ -16,6 +16,7 @@
 #include <cmath>
 
 #include "inl_common.hpp"
+#include "lanes.hpp"
 
 namespace inl {
 
@@ -29,7 +30,7 @@ __device__ __forceinline__ float ld(const char* p) {
 
 // Sum of `v` over the block (blockDim.x <= 1024, multiple of 64).
 __device__ float block_sum(float v, float* red) {
-  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  v = wave_sum(v);
   const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[w] = v;
