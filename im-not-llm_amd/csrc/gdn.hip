@@ -52,12 +52,27 @@ __device__ __forceinline__ float div_t(float x, float d) {
   else return __fdiv_rn(x, d);
 }
 
+// Two f32 values rounded to bf16 and back with one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ void rnd2_bf16(float a, float b, float& ra, float& rb) {
+  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  ra = __builtin_bit_cast(float, h << 16);
+  rb = __builtin_bit_cast(float, h & 0xffff0000u);
+}
+
 // candle's silu with every step rounded in T: x / (1 + exp(-x)).
 template <typename T>
 __device__ __forceinline__ float silu_t(float x) {
   const float e = rnd<T>(exp_t<T>(rnd<T>(-x)));
   const float d = rnd<T>(1.0f + e);
   return rnd<T>(div_t<T>(x, d));
+}
+// silu_t<bf16> of two values that are bf16 already (so -x needs no rounding),
+// each rounding of the pair one conversion.
+__device__ __forceinline__ void silu2_bf16(float x0, float x1, float& y0, float& y1) {
+  float e0, e1, d0, d1;
+  rnd2_bf16(exp_t<bf16>(-x0), exp_t<bf16>(-x1), e0, e1);
+  rnd2_bf16(1.0f + e0, 1.0f + e1, d0, d1);
+  rnd2_bf16(div_t<bf16>(x0, d0), div_t<bf16>(x1, d1), y0, y1);
 }
 
 // Index of the text holding packed row t: the last b with cu[b] <= t
@@ -125,7 +140,22 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const T* __restrict__ x, 
   }
 
   const int64_t t1 = t0 + CONV_RUN < n_tokens ? t0 + CONV_RUN : n_tokens;
-  for (int64_t t = t0; t < t1; ++t) {
+  // Every row of the run is loaded first (rows past the end at the run's
+  // last row, unused), so the loads are in flight together; the unrolled
+  // loop then renames the window registers instead of moving them.
+  constexpr bool VB = V == 8 && sizeof(T) == 2, VF = V == 4 && sizeof(T) == 4;
+  u32x4 raw[VB ? CONV_RUN : 1];
+  f32x4 rawf[VF ? CONV_RUN : 1];
+#pragma unroll
+  for (int i = 0; i < CONV_RUN; ++i) {
+    const int64_t tc = t0 + i < t1 ? t0 + i : t1 - 1;
+    if constexpr (VB) raw[i] = *reinterpret_cast<const u32x4*>(x + tc * xs + c0);
+    if constexpr (VF) rawf[i] = *reinterpret_cast<const f32x4*>(x + tc * xs + c0);
+  }
+#pragma unroll
+  for (int i = 0; i < CONV_RUN; ++i) {
+    const int64_t t = t0 + i;
+    if (t >= t1) break;
     if (t >= stop) {  // the next text starts here: zero padding again
       while (t >= stop && b + 1 < n_texts) { ++b; stop = at(b + 1); }
       start = t < stop ? at(b) : t;  // rows past cu[n_texts] start afresh
@@ -135,30 +165,46 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const T* __restrict__ x, 
         for (int e = 0; e < V; ++e) win[j][e] = 0.f;
     }
     float cur[V];
-    if constexpr (V == 8 && sizeof(T) == 2) {
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(x + t * xs + c0);
+    if constexpr (VB) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) cur[e] = (float)v[e];
-    } else if constexpr (V == 4 && sizeof(T) == 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(x + t * xs + c0);
+      for (int e = 0; e < 8; ++e)
+        cur[e] = __builtin_bit_cast(float, (e & 1) ? (raw[i][e >> 1] & 0xffff0000u) : (raw[i][e >> 1] << 16));
+    } else if constexpr (VF) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) cur[e] = v[e];
+      for (int e = 0; e < 4; ++e) cur[e] = rawf[i][e];
     } else {
 #pragma unroll
       for (int e = 0; e < V; ++e) cur[e] = ld1(x + t * xs + c0 + e);
     }
     float res[V];
+    if constexpr (sizeof(T) == 2 && V % 2 == 0) {
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      // tap k reads row t + k - (TAPS - 1): win[TAPS - 2 - k], the last tap cur
-      float acc = 0.f;
+      for (int e = 0; e < V; e += 2) {
+        // tap k reads row t + k - (TAPS - 1): win[TAPS - 2 - k], the last tap cur
+        float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-      for (int k = 0; k < TAPS; ++k) {
-        const float s = k == TAPS - 1 ? cur[e] : win[TAPS - 2 - k][e];
-        const float term = rnd<T>(s * wt[k][e]);
-        acc = rnd<T>(acc + term);
+        for (int k = 0; k < TAPS; ++k) {
+          const float s0 = k == TAPS - 1 ? cur[e] : win[TAPS - 2 - k][e];
+          const float s1 = k == TAPS - 1 ? cur[e + 1] : win[TAPS - 2 - k][e + 1];
+          float p0, p1;
+          rnd2_bf16(s0 * wt[k][e], s1 * wt[k][e + 1], p0, p1);
+          rnd2_bf16(a0 + p0, a1 + p1, a0, a1);
+        }
+        silu2_bf16(a0, a1, res[e], res[e + 1]);
       }
-      res[e] = silu_t<T>(acc);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        // tap k reads row t + k - (TAPS - 1): win[TAPS - 2 - k], the last tap cur
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < TAPS; ++k) {
+          const float s = k == TAPS - 1 ? cur[e] : win[TAPS - 2 - k][e];
+          const float term = rnd<T>(s * wt[k][e]);
+          acc = rnd<T>(acc + term);
+        }
+        res[e] = silu_t<T>(acc);
+      }
     }
 #pragma unroll
     for (int j = TAPS - 2; j > 0; --j)
@@ -166,12 +212,13 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const T* __restrict__ x, 
       for (int e = 0; e < V; ++e) win[j][e] = win[j - 1][e];
 #pragma unroll
     for (int e = 0; e < V; ++e) win[0][e] = cur[e];
-    if constexpr (V == 8 && sizeof(T) == 2) {
-      bf16x8 v;
+    if constexpr (VB) {
+      u32x4 o;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (bf16)res[e];
-      *reinterpret_cast<bf16x8*>(out + t * os + c0) = v;
-    } else if constexpr (V == 4 && sizeof(T) == 4) {
+      for (int q = 0; q < 4; ++q)
+        o[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){res[2 * q], res[2 * q + 1]}, bf16x2));
+      *reinterpret_cast<u32x4*>(out + t * os + c0) = o;
+    } else if constexpr (VF) {
       f32x4 v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = res[e];
