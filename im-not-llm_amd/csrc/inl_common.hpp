@@ -44,4 +44,10 @@ int set_max_dynamic_lds(const void* fn, int bytes);
 // count through `total`.
 int check_cu(int32_t n, const int32_t* cu, int64_t* total);
 
+// inl_norm_rope_fwd with heads >= w2_heads (a multiple of 4) normalised with
+// weight2: the q and k heads of one fused QKV row in one launch.
+int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const void* weight,
+                     const void* weight2, int32_t w2_heads, const int32_t* rows, const float* cos,
+                     const float* sin, const float* cos2, const float* sin2, void* stream);
+
 }  // namespace inl

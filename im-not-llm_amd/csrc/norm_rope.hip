@@ -27,6 +27,8 @@ struct NormRopeParams {
   const char* x;
   char* y;
   const char* w;            // [head_dim] in x dtype, or null
+  const char* w2;           // heads >= w2_heads use this weight instead (null: none)
+  int32_t w2_heads;
   const int32_t* rows;      // table row per token
   const float* cos;
   const float* sin;
@@ -164,7 +166,8 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
   float w[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) w[e] = 1.f;
-  if (p.norm && p.w) load8<TI>(p.w + 8 * j * (int)sizeof(TI), w);
+  const char* wsel = p.w2 && hfirst >= p.w2_heads ? p.w2 : p.w;
+  if (p.norm && wsel) load8<TI>(wsel + 8 * j * (int)sizeof(TI), w);
 
   // rope geometry: `mode` 0 = none for this lane, 1 = pairs (e, e + 4) inside
   // the lane (rotary_dim 8), 2 = half-split with the partner lane
@@ -282,11 +285,13 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
 
 }  // namespace inl
 
-extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, void* y,
-                                 const void* weight, const int32_t* rows, const float* cos,
-                                 const float* sin, const float* cos2, const float* sin2,
-                                 void* stream) {
-  using namespace inl;
+namespace inl {
+
+// inl_norm_rope_fwd, with heads >= w2_heads (a multiple of the kernel's
+// 4-head step) normalised with weight2 instead of weight.
+int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const void* weight,
+                     const void* weight2, int32_t w2_heads, const int32_t* rows, const float* cos,
+                     const float* sin, const float* cos2, const float* sin2, void* stream) {
   if (!d) return fail(INL_E_INVALID, "norm_rope: desc is NULL");
   if (!dtype_ok(d->dtype) || !dtype_ok(d->out_dtype))
     return fail(INL_E_INVALID, "norm_rope: dtype must be INL_F32 or INL_BF16");
@@ -317,13 +322,18 @@ extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, voi
       (ys * dtype_size(d->out_dtype)) % 16)
     return fail(INL_E_INVALID, "norm_rope: row strides must cover all heads, in 16-byte multiples");
   if (d->n_tokens == 0) return INL_OK;
-  if (!x || !y || ((uintptr_t)x & 15) || ((uintptr_t)y & 15) || (weight && ((uintptr_t)weight & 15)))
+  if (!x || !y || ((uintptr_t)x & 15) || ((uintptr_t)y & 15) || (weight && ((uintptr_t)weight & 15)) ||
+      (weight2 && ((uintptr_t)weight2 & 15)))
     return fail(INL_E_INVALID, "norm_rope: x, y and weight must be non-null and 16-byte aligned");
+  if (weight2 && (w2_heads <= 0 || w2_heads % 4 || w2_heads >= d->heads))
+    return fail(INL_E_INVALID, "norm_rope: the second weight's first head must be a multiple of 4 inside the heads");
 
   NormRopeParams p{};
   p.x = (const char*)x;
   p.y = (char*)y;
   p.w = d->norm ? (const char*)weight : nullptr;
+  p.w2 = d->norm ? (const char*)weight2 : nullptr;
+  p.w2_heads = weight2 ? w2_heads : 0;
   p.rows = rows;
   p.cos = cos;
   p.sin = sin;
@@ -369,6 +379,15 @@ extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, voi
   else launch(float{}, float{});
   INL_HIP_TRY(hipGetLastError());
   return INL_OK;
+}
+
+}  // namespace inl
+
+extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, void* y,
+                                 const void* weight, const int32_t* rows, const float* cos,
+                                 const float* sin, const float* cos2, const float* sin2,
+                                 void* stream) {
+  return inl::norm_rope_launch(d, x, y, weight, nullptr, 0, rows, cos, sin, cos2, sin2, stream);
 }
 
 extern "C" int inl_rope_table_host(int32_t rotary_dim, double theta, int32_t positions,

@@ -7,7 +7,8 @@
 //   per layer (DecoderLayer::forward, :280-297):
 //     x   = rms_norm(residual) * input_norm                 (inl_rms_norm_rows_fwd)
 //     qkv = x . [Wq; Wk; Wv]^T                              (inl_linear_fwd)
-//     q, k = rope(rms_norm(q|k) * q|k_norm), in place        (inl_norm_rope_fwd)
+//     q, k = rope(rms_norm(q|k) * q|k_norm), in place        (inl_norm_rope_fwd: q and k
+//                                                             heads in one launch)
 //     a   = causal GQA attention over the texts             (inl_attn_fwd)
 //     residual += a . Wo^T                                  (inl_linear_fwd, beta 1)
 //     x   = rms_norm(residual) * post_attention_norm
@@ -381,14 +382,19 @@ extern "C" int inl_qwen3_encode(inl_qwen3* e, int32_t n_texts, const int32_t* cu
     rc = inl_rms_norm_rows_fwd(n, c.hidden, resid, c.hidden, w.input_norm, dt, c.eps, dt, x, c.hidden, stream);
     if (!rc) rc = inl_linear_fwd(n, qkv_w, c.hidden, dt, x, c.hidden, w.qkv_proj, c.hidden, dt, A, L.a_w, 1.f, 0.f,
                                  gws, gws_bytes, stream);
-    if (!rc) {
+    if (!rc && c.heads % 4 == 0) {
+      // q and k heads are adjacent in the QKV row: one launch, k_norm from head `heads` on
+      nr.heads = c.heads + c.kv_heads;
+      rc = norm_rope_launch(&nr, A, A, w.q_norm, w.k_norm, c.heads, d_pos, e->cos, e->sin, nullptr, nullptr,
+                            stream);
+    } else if (!rc) {
       nr.heads = c.heads;
       rc = inl_norm_rope_fwd(&nr, A, A, w.q_norm, d_pos, e->cos, e->sin, nullptr, nullptr, stream);
-    }
-    if (!rc) {
-      nr.heads = c.kv_heads;
-      rc = inl_norm_rope_fwd(&nr, A + qd * es, A + qd * es, w.k_norm, d_pos, e->cos, e->sin, nullptr, nullptr,
-                             stream);
+      if (!rc) {
+        nr.heads = c.kv_heads;
+        rc = inl_norm_rope_fwd(&nr, A + qd * es, A + qd * es, w.k_norm, d_pos, e->cos, e->sin, nullptr, nullptr,
+                               stream);
+      }
     }
     if (!rc) rc = inl_attn_fwd(plan, A, A + qd * es, A + (qd + kvd) * es, B, stream);
     if (!rc) rc = inl_linear_fwd(n, c.hidden, qd, dt, B, L.b_w, w.o_proj, qd, INL_F32, resid, c.hidden, 1.f, 1.f,
