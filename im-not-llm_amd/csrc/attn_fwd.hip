@@ -559,6 +559,29 @@ struct KernelCfg {
   const char* name = "";    // kernel name, for reporting
 };
 
+int unit_weight(const KernelCfg& cfg, const inl_attn_desc* d, int T, int q0, int BM, int lo_t, int hi_t) {
+  const int tiles = hi_t - lo_t;
+  if (!cfg.persistent) return 8 * tiles + 18;
+  const int BN = cfg.bn;
+  const int rows = std::min(T, q0 + BM) - q0;
+  int masked = 0;
+  for (int t = lo_t; t < hi_t; ++t) {
+    bool need = false;
+    for (int r0 = q0; r0 < q0 + BM && !need; r0 += 32) {
+      if (r0 >= T) { need = true; break; }
+      const int rlast = std::min(r0 + 31, T - 1);
+      int e = T;
+      if (d->causal) e = std::min(e, r0 + 1);
+      if (d->window >= 0) e = std::min(e, r0 + d->window + 1);
+      const int f_hi = e / BN;
+      const int f_lo = d->window >= 0 ? (std::max(0, rlast - d->window) + BN - 1) / BN : 0;
+      need = t < f_lo || t >= f_hi;
+    }
+    masked += need;
+  }
+  return 8 * tiles + 17 + 3 * masked + (rows * 35 + 512) / 1024;
+}
+
 template <typename E, int D, int BN, int NW, bool PV16>
 KernelCfg make_cfg(const char* name) {
   return KernelCfg{attn_fwd_kernel<E, D, BN, NW, PV16>, D, BN, NW, 4 * BN * D * (int)sizeof(E), 32, false, false,
@@ -734,16 +757,27 @@ int device_cus() {
   return n;
 }
 
+// Expected time of one persistent unit (text of T rows, query rows q0 ..
+// q0 + BM - 1, key tiles lo_t .. hi_t - 1), in eighths of a key tile: a
+// tile, 2.1 tiles per unit (Q in, O out, the switch), 0.4 per tile on which
+// some 32-row wave needs a mask, and 0.55 per 128 query rows inside the
+// text. Fitted (least squares, 2.8 % rms) to per-workgroup cycle counts of
+// attn_pp over mixed-length causal and windowed batches; the weights also
+// balance attn_pp64 better than tiles + 2.25 per unit and are neutral for
+// attn_wide.
+struct KernelCfg;
+int unit_weight(const KernelCfg& cfg, const inl_attn_desc* d, int T, int q0, int BM, int lo_t, int hi_t);
+
 struct CostedItem {
   int4 it;
-  int cost;  // key tiles
+  int cost;        // key tiles
+  int weight = 0;  // persistent kernels: expected time of one unit, in eighths of a tile
 };
 
 // Persistent schedule (`gpk`: head groups per KV head, consecutive in hg):
 // every (item, head group) unit goes to the workgroup
-// with the least work so far (longest units first, LPT). A workgroup costs
-// its tiles plus the per-unit overhead (Q load, output store, first-tile
-// set-up), measured at about 2.3 tiles of head_dim 128 work per unit.
+// with the least work so far (longest units first, LPT), by the units'
+// weights (unit_weight: tiles plus per-unit overhead).
 // Workgroups are dispatched to the 8 XCDs round-robin (b % 8), and each XCD
 // has its own L2; when the head groups split evenly over the XCDs, units of
 // head group h run only on workgroups b with b % 8 == h % 8, so the K/V rows
@@ -780,7 +814,7 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
       std::vector<int64_t> seg_units(n_streams, 0);
       for (size_t i = 0; i < items.size(); ++i)
         for (int kv = 0; kv < n_kv; ++kv) {
-          seg_cost[(int64_t)text_of[i] * n_kv + kv] += (int64_t)gpk * (4 * items[i].cost + 9);
+          seg_cost[(int64_t)text_of[i] * n_kv + kv] += (int64_t)gpk * items[i].weight;
           seg_units[(int64_t)text_of[i] * n_kv + kv] += gpk;
         }
       std::vector<int64_t> order(n_streams);
@@ -815,7 +849,7 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
     Load top = h.top();
     h.pop();
     lists[top.second].push_back((int64_t)i * n_hg + hg);
-    if ((int)lists[top.second].size() < PP_MAX_UNITS) h.push(Load(top.first + 4 * items[i].cost + 9, top.second));
+    if ((int)lists[top.second].size() < PP_MAX_UNITS) h.push(Load(top.first + items[i].weight, top.second));
   };
   // Texts in groups of about one unit per workgroup (texts by total cost,
   // longest first), each group longest unit first. The q-blocks of a text
@@ -827,7 +861,7 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
   std::vector<int64_t> text_cost(n_texts, 0);
   std::vector<std::vector<size_t>> text_items(n_texts);
   for (size_t i = 0; i < items.size(); ++i) {
-    text_cost[text_of[i]] += items[i].cost;
+    text_cost[text_of[i]] += items[i].weight;
     text_items[text_of[i]].push_back(i);
   }
   std::vector<int> text_order(n_texts);
@@ -998,7 +1032,8 @@ int build_schedule(const inl_attn_desc* d, Schedule* s, bool allow_split = true)
       const int lo_t = lo / BN, hi_t = (hi + BN - 1) / BN;
       if (hi_t > 0xffff)
         return fail(INL_E_UNSUPPORTED, "attention: a text spans more than 65535 key tiles");
-      tmp.push_back({make_int4(seg, T, q0, (lo_t << 16) | hi_t), hi_t - lo_t});
+      tmp.push_back({make_int4(seg, T, q0, (lo_t << 16) | hi_t), hi_t - lo_t,
+                     unit_weight(s->cfg, d, T, q0, BM, lo_t, hi_t)});
     }
   }
   std::stable_sort(tmp.begin(), tmp.end(),
