@@ -334,6 +334,7 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
   // row at a time (chunk c of row r at r * 128 + ((c ^ (r & 7)) << 4)), so
   // that each store writes 8 whole 128-byte lines. `stg`: 4 KB of LDS that
   // no other wave touches during this step.
+  // The stores are non-temporal (nt): nothing in the launch reads O.
   auto store_out = [&](uint32_t stg) __attribute__((always_inline)) {
     const float l_tot = l_i;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -359,7 +360,7 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           __builtin_amdgcn_raw_buffer_store_b128(lds_load<u32x4>(rd + j * 8 * 128), ors,
-                                                 o_off + j * 8 * ost_b + part * 128, 0, 0);
+                                                 o_off + j * 8 * ost_b + part * 128, 0, 2);
       }
     } else {
 #pragma unroll
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
           u32x4 val;
 #pragma unroll
           for (int e = 0; e < 4; ++e) val[e] = __builtin_bit_cast(uint32_t, oacc[db][4 * g + e] * inv);
-          __builtin_amdgcn_raw_buffer_store_b128(val, ors, o_off + (db * 32 + 8 * g) * 4, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(val, ors, o_off + (db * 32 + 8 * g) * 4, 0, 2);
         }
     }
 #pragma unroll
