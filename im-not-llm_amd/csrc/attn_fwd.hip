@@ -794,10 +794,10 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
   n_wg = std::max<int64_t>(n_wg, (U + PP_MAX_UNITS - 1) / PP_MAX_UNITS);
   n_wg = (n_wg + 7) / 8 * 8;
   // Stream affinity: without head-group affinity, each (text, KV head)
-  // stream goes to one XCD class (streams longest-first to the class with
-  // the least work), so the q-blocks that re-read a stream's K/V rows share
-  // one L2. Used when there are enough streams to balance the 8 classes and
-  // no class outgrows its workgroups' unit tables.
+  // stream, or each piece of a long one, goes to one XCD class (longest
+  // first to the class with the least work), so the q-blocks that re-read
+  // its K/V rows share one L2. Used when there are enough streams, the
+  // classes balance, and no class outgrows its workgroups' unit tables.
   const int n_kv = n_hg / gpk;
   std::vector<int> text_of(items.size());
   std::unordered_map<int, int> text_id;   // text start row -> text number, in first-seen order
@@ -807,35 +807,65 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
   std::vector<int> stream_class;
   bool streams = false;
   if (!affinity && n_wg >= 8 && (int64_t)items.size() * n_kv >= 32) {
-    std::vector<int64_t> seg_cost;   // per (text, KV head)
     const int64_t n_streams = (int64_t)n_texts * n_kv;
     if (n_streams >= 32) {
-      seg_cost.assign(n_streams, 0);
-      std::vector<int64_t> seg_units(n_streams, 0);
-      for (size_t i = 0; i < items.size(); ++i)
+      // Streams in pieces of contiguous query blocks, each at most half a
+      // class's share of the work: one long text then spreads over several
+      // XCDs instead of overloading one (its K/V rows are re-read per piece,
+      // which a sliding window mostly confines to the piece's own rows).
+      std::vector<std::vector<size_t>> text_items(n_texts);
+      int64_t total = 0;
+      for (size_t i = 0; i < items.size(); ++i) {
+        text_items[text_of[i]].push_back(i);
+        total += (int64_t)n_kv * gpk * items[i].weight;
+      }
+      const int64_t cap = std::max<int64_t>(1, total / 16);
+      std::vector<int64_t> piece_cost, piece_units;
+      std::vector<int64_t> piece_of(items.size() * n_kv);
+      for (int t = 0; t < n_texts; ++t) {
+        std::vector<size_t>& ti = text_items[t];
+        std::stable_sort(ti.begin(), ti.end(), [&](size_t a, size_t b) { return items[a].it.z < items[b].it.z; });
         for (int kv = 0; kv < n_kv; ++kv) {
-          seg_cost[(int64_t)text_of[i] * n_kv + kv] += (int64_t)gpk * items[i].weight;
-          seg_units[(int64_t)text_of[i] * n_kv + kv] += gpk;
+          int64_t acc = 0;
+          for (size_t i : ti) {
+            const int64_t c = (int64_t)gpk * items[i].weight;
+            if (acc == 0 || acc + c > cap) {
+              piece_cost.push_back(0);
+              piece_units.push_back(0);
+              acc = 0;
+            }
+            acc += c;
+            piece_cost.back() += c;
+            piece_units.back() += gpk;
+            piece_of[i * n_kv + kv] = (int64_t)piece_cost.size() - 1;
+          }
         }
-      std::vector<int64_t> order(n_streams);
-      for (int64_t k = 0; k < n_streams; ++k) order[k] = k;
-      std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return seg_cost[a] > seg_cost[b]; });
-      std::vector<int> cls(n_streams);
-      std::vector<int64_t> cls_units(8, 0);
+      }
+      const int64_t n_pieces = (int64_t)piece_cost.size();
+      std::vector<int64_t> order(n_pieces);
+      for (int64_t k = 0; k < n_pieces; ++k) order[k] = k;
+      std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return piece_cost[a] > piece_cost[b]; });
+      std::vector<int> cls(n_pieces);
+      std::vector<int64_t> cls_units(8, 0), cls_cost(8, 0);
       std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>, std::greater<std::pair<int64_t, int>>> ch;
       for (int c = 0; c < 8; ++c) ch.push({0, c});
       for (int64_t k : order) {
         auto top = ch.top();
         ch.pop();
         cls[k] = top.second;
-        cls_units[top.second] += seg_units[k];
-        ch.push({top.first + seg_cost[k], top.second});
+        cls_units[top.second] += piece_units[k];
+        cls_cost[top.second] = top.first + piece_cost[k];
+        ch.push({top.first + piece_cost[k], top.second});
       }
-      streams = *std::max_element(cls_units.begin(), cls_units.end()) <= (n_wg / 8) * (int64_t)PP_MAX_UNITS;
+      // Classes must fit their workgroups' unit tables and balance within
+      // 10 %; otherwise no stream affinity.
+      const int64_t cmax = *std::max_element(cls_cost.begin(), cls_cost.end());
+      streams = *std::max_element(cls_units.begin(), cls_units.end()) <= (n_wg / 8) * (int64_t)PP_MAX_UNITS &&
+                cmax * 8 * 10 <= total * 11;
       if (streams) {
         stream_class.resize(items.size() * n_kv);
         for (size_t i = 0; i < items.size(); ++i)
-          for (int kv = 0; kv < n_kv; ++kv) stream_class[i * n_kv + kv] = cls[(int64_t)text_of[i] * n_kv + kv];
+          for (int kv = 0; kv < n_kv; ++kv) stream_class[i * n_kv + kv] = cls[piece_of[i * n_kv + kv]];
       }
     }
   }

@@ -16,7 +16,17 @@ pytestmark = pytest.mark.gpu
 
 
 CASES = ["config2_all_in_one_launch", "qwen3_2048_causal", "gemma_window512", "gemma_full",
-         "modernbert_local64", "modernbert_global", "pplx_causal", "vision"]
+         "modernbert_local64", "modernbert_global", "pplx_causal", "vision",
+         "gemma_full_long_in_mix", "pplx_causal_mix"]
+
+
+def _mix(n, median, longest, seed):
+    """Log-normal lengths (sigma 1) with one text of ``longest`` rows: the
+    planner splits that text's (text, KV head) stream over several XCDs."""
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in np.clip(rng.lognormal(np.log(median), 1.0, n), 16, longest)]
+    lens[n // 3] = longest
+    return lens
 
 
 def _case(name):
@@ -32,6 +42,8 @@ def _case(name):
         "modernbert_global": (w.uniform_lengths(128, 32, 2048), 12, 12, 64, False, -1),
         "pplx_causal": ([4096] * 16, 16, 2, 256, True, -1),
         "vision": ([256] * 64, 16, 16, 64, False, -1),
+        "gemma_full_long_in_mix": (_mix(48, 600, 8192, 100), 3, 1, 256, False, -1),
+        "pplx_causal_mix": (_mix(32, 1000, 8192, 101), 16, 2, 256, True, -1),
     }[name]
 
 
@@ -128,7 +140,8 @@ def _textbook_rows(qrows, kh, vh, lengths, rows, hq, hkv, causal, window, scale)
 
 
 SAMPLED = [(c, "bf16") for c in ("config2_all_in_one_launch", "qwen3_2048_causal", "gemma_window512",
-                                 "gemma_full", "modernbert_local64", "modernbert_global", "pplx_causal")] + \
+                                 "gemma_full", "modernbert_local64", "modernbert_global", "pplx_causal",
+                                 "gemma_full_long_in_mix", "pplx_causal_mix")] + \
           [(c, "f32") for c in ("modernbert_local64", "modernbert_global")]
 
 
