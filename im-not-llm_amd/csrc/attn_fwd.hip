@@ -579,6 +579,7 @@ int unit_weight(const KernelCfg& cfg, const inl_attn_desc* d, int T, int q0, int
     }
     masked += need;
   }
+  if (cfg.d == 256) return 8 * tiles + 46 + masked + (rows * 7 + 32) / 64;
   return 8 * tiles + 17 + 3 * masked + (rows * 35 + 512) / 1024;
 }
 
@@ -762,9 +763,10 @@ int device_cus() {
 // tile, 2.1 tiles per unit (Q in, O out, the switch), 0.4 per tile on which
 // some 32-row wave needs a mask, and 0.55 per 128 query rows inside the
 // text. Fitted (least squares, 2.8 % rms) to per-workgroup cycle counts of
-// attn_pp over mixed-length causal and windowed batches; the weights also
-// balance attn_pp64 better than tiles + 2.25 per unit and are neutral for
-// attn_wide.
+// attn_pp over mixed-length causal and windowed batches; attn_pp64's own fit
+// (1.4 % rms) is close to them. attn_wide (head_dim 256, 32-key tiles) has
+// its own: 5.75 tiles per unit, 0.17 per masked tile and 1.75 per 128 rows
+// (2.5 % rms).
 struct KernelCfg;
 int unit_weight(const KernelCfg& cfg, const inl_attn_desc* d, int T, int q0, int BM, int lo_t, int hi_t);
 
