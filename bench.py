@@ -36,7 +36,10 @@ the bf16 MFMA peak and gdn_rule (f32 vector work) against the 157.3 TFLOP/s
 fp32 vector peak. The
 end-to-end workloads (--workload qwen3_e2e, f32 as configuration 1, and
 qwen3_e2e_bf16) time a whole Qwen3-0.6B encode of 8 texts (778 tokens) and
-report encoded tokens/s, with the numpy f32 forward as the CPU baseline.
+report encoded tokens/s, with the numpy f32 forward as the CPU baseline;
+--workload gemma_e2e would do the same for configuration 3 (the
+EmbeddingGemma-2 text tower, bf16, 32 texts of U[64,8192] tokens); it is
+switched off for now (see gemma_e2e_main).
 """
 from __future__ import annotations
 
@@ -298,6 +301,113 @@ def e2e_main(args):
     print(json.dumps(result), flush=True)
 
 
+def gemma_e2e_cpu_baseline(host_w, tc, seconds):
+    """The oracle's numpy EmbeddingGemma 2 forward (oracle/gemma2.py) in f32
+    on the host cores (the reference's CPU path is f32: bf16 is refused on
+    the CPU, gemma2.rs:685-691), over the benchmark's weights and a bounded
+    sample of 4 texts of U[64, 512] tokens, repeated until `seconds`."""
+    import numpy as np
+    from oracle import gemma2 as og
+    from inl_hip import workloads as w
+    lengths = w.uniform_lengths(4, 64, 512, seed=1)
+    cu = np.asarray(w.cu_seqlens(lengths))
+    ids = np.random.default_rng(1).integers(0, tc["vocab_size"], int(cu[-1]))
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
+    except Exception:
+        cores = os.cpu_count() or 1
+    spent, runs = 0.0, 0
+    while spent < seconds or runs == 0:
+        t0 = time.perf_counter()
+        og.encode(host_w, tc, ids, cu, dtype=np.float32)
+        spent += time.perf_counter() - t0
+        runs += 1
+    tokens = int(cu[-1]) * runs
+    return {"value": round(tokens / spent, 1), "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": (f"{runs} encodes of 4 texts U[64,512] ({int(cu[-1])} tokens each) through oracle/gemma2.py "
+                       f"(numpy f32 forward: BLAS GEMMs, per-text attention) with the same weights, {spent:.2f} s")}
+
+
+def gemma_e2e_main(args):
+    """Configuration 3 end to end: the EmbeddingGemma-2 text tower of
+    gemma2.rs at the benchmark's shape (24 layers, hidden 768, 3 Q / 1 KV
+    heads x 256, sliding radius 512 with every sixth layer full) on 32 texts
+    of U[64, 8192] tokens, bf16; embed -> per-layer inputs -> 24 layers ->
+    mean pool -> projection -> L2; one step = one encode."""
+    # Switched off: the one full-size run (139,124 tokens) ended in a GPU memory
+    # fault, after hipBLASLt printed "Could not initialize Tensile host:
+    # unordered_map::at" and before any step completed. The runner's tests at
+    # smaller sizes pass; no cause in this library's code has been found yet,
+    # so the full-size encode stays off the GPU until one is.
+    raise SystemExit("bench.py: --workload gemma_e2e is switched off: its full-size encode faulted the GPU "
+                     "once and the cause is not found yet")
+    import numpy as np
+    import torch
+    import inl_hip
+    from inl_hip import workloads as w
+    dev = torch.device("cuda:0")
+    tc = w.gemma2_config3()
+    host_w = w.gemma2_random_weights(tc, seed=0)
+    weights = {k: torch.from_numpy(v).to(dev).to(torch.bfloat16) for k, v in host_w.items()}
+    lengths = w.uniform_lengths(32, 64, 8192)
+    cu = np.asarray(w.cu_seqlens(lengths))
+    tokens = int(cu[-1])
+    ids = np.random.default_rng(0).integers(0, tc["vocab_size"], tokens).astype(np.int32)
+    enc = inl_hip.Gemma2Encoder(tc, weights, max_positions=8192)
+    out = torch.empty((len(lengths), tc["embedding_dim"]), dtype=torch.float32, device=dev)
+    ws = torch.empty(enc.workspace_bytes(cu.tolist()) + 256, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    H, I, E, heads, hd, kvh = (tc["hidden_size"], tc["intermediate_size"], tc["hidden_size_per_layer_input"],
+                               tc["num_attention_heads"], tc["head_dim"], tc["num_key_value_heads"])
+    per_token = 2 * (H * (heads + 2 * kvh) * hd + heads * hd * H + 2 * H * I + I * H + 3 * H * E)
+    flops = 0
+    for kind in tc["layer_types"]:
+        window = tc["sliding_window"] if kind == "sliding_attention" else -1
+        flops += tokens * per_token + inl_hip.attention_flops(lengths, heads, hd, False, window)
+    label = (f"config3: EmbeddingGemma-2 text tower end to end (bf16): 24 layers (every sixth full), hidden 768, "
+             f"3 Q / 1 KV heads x 256, sliding radius 512, intermediate 1152, per-layer input 256, embedding_dim 768, "
+             f"vocab 262144; mean pooling, projection, L2; 32 texts U[64,8192] = {tokens} tokens, random ids, "
+             f"random-init weights")
+    log(f"workload: {label}; {flops / 1e12:.3f} TFLOP per encode")
+
+    def step(evs=None):
+        if evs is not None:
+            evs[0][0].record(stream)
+        enc.encode(ids, cu.tolist(), out=out, workspace=ws, stream=stream)
+        if evs is not None:
+            evs[0][1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    avg_ms = timed_launches(torch, step, 1, args.steps)
+    ach = flops / (avg_ms * 1e-3) / 1e12
+    result = {
+        "metric": METRIC, "value": round(tokens * args.steps / wall, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random token ids, seeded random-init weights; no checkpoint)",
+        "config": {"workload": label, "tokens_per_step": tokens, "texts": len(lengths),
+                   "tflop_per_step": round(flops / 1e12, 6),
+                   "value_is": "end-to-end encoded tokens/s (embed, 24 layers, pooling, projection, L2 per step)"},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "whole encode (hipBLASLt GEMMs, attention, prologue, norms, GEGLU, pooling)",
+                     "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"flop": flops}},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = gemma_e2e_cpu_baseline(host_w, tc, args.cpu_seconds)
+    enc.close()
+    print(json.dumps(result), flush=True)
+
+
 def op_workload(name, torch, inl_hip, dev):
     """The prologue and epilogue kernels at their configurations' full sizes.
     Returns (label, kernel, launches per step, step(evs), tokens per step,
@@ -537,6 +647,9 @@ def main():
 
     if args.workload in OP_WORKLOADS:
         op_main(args)
+        return
+    if args.workload == "gemma_e2e":
+        gemma_e2e_main(args)
         return
     if args.workload in E2E_WORKLOADS:
         e2e_main(args)

@@ -681,6 +681,130 @@ class Qwen3Encoder:
             pass
 
 
+class Gemma2Config(ctypes.Structure):
+    _fields_ = [("vocab", c_i32), ("hidden", c_i32), ("intermediate", c_i32), ("layers", c_i32),
+                ("heads", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32), ("ple_dim", c_i32),
+                ("embedding_dim", c_i32), ("sliding_window", c_i32), ("eps", ctypes.c_float),
+                ("theta_sliding", ctypes.c_double), ("theta_full", ctypes.c_double), ("max_positions", c_i32),
+                ("dtype", c_i32), ("attn_flags", c_i32)]
+
+
+_G2_WEIGHTS = ("qkv_proj", "o_proj", "gate_up_proj", "down_proj", "q_norm", "k_norm", "input_norm",
+               "post_attention_norm", "pre_feedforward_norm", "post_feedforward_norm", "ple_input_gate",
+               "ple_projection", "ple_post_norm", "layer_scalar")
+
+
+class Gemma2LayerWeights(ctypes.Structure):
+    _fields_ = [("full", c_i32), ("head_dim", c_i32), ("kv_heads", c_i32)] + [(n, c_void_p) for n in _G2_WEIGHTS]
+
+
+_g2_create = _sig("inl_gemma2_create", ctypes.c_int, ctypes.POINTER(Gemma2Config), c_void_p,
+                  ctypes.POINTER(Gemma2LayerWeights), c_void_p, c_void_p, c_void_p, c_void_p, ctypes.POINTER(c_void_p))
+_g2_destroy = _sig("inl_gemma2_destroy", ctypes.c_int, c_void_p)
+_g2_ws = _sig("inl_gemma2_workspace_size", ctypes.c_int, c_void_p, c_i32, c_void_p, ctypes.POINTER(ctypes.c_size_t))
+_g2_encode = _sig("inl_gemma2_encode", ctypes.c_int, c_void_p, c_i32, c_void_p, c_void_p, c_i32, c_void_p, c_void_p,
+                  ctypes.c_size_t, c_void_p)
+
+
+class Gemma2Encoder:
+    """The GPU EmbeddingGemma 2 text tower (``inl_gemma2_*``): packed texts
+    in, unit-length mean-pooled embeddings out. ``text_config`` is the
+    checkpoint's ``text_config`` dict (``layer_types``, ``per_layer_config``,
+    ``rope_parameters``, ...); ``weights`` maps the text model's tensor names
+    (``embed_tokens.weight``, ``layers.{i}.self_attn.q_proj.weight``, ...,
+    ``ple.per_layer_model_projection.weight``, ``embedding_projection.weight``)
+    to device tensors of one dtype. q/k/v and gate/up are stacked once here."""
+
+    def __init__(self, text_config, weights, *, max_positions=None, attn_flags=0):
+        import torch
+        tc = text_config
+        t0 = weights["embed_tokens.weight"]
+        self.dtype = t0.dtype
+        self.embedding_dim = int(tc["embedding_dim"])
+        c = Gemma2Config()
+        c.vocab, c.hidden, c.intermediate = tc["vocab_size"], tc["hidden_size"], tc["intermediate_size"]
+        c.layers, c.heads, c.kv_heads = tc["num_hidden_layers"], tc["num_attention_heads"], tc["num_key_value_heads"]
+        c.head_dim, c.ple_dim, c.embedding_dim = tc["head_dim"], tc["hidden_size_per_layer_input"], tc["embedding_dim"]
+        c.sliding_window, c.eps = tc["sliding_window"], tc["rms_norm_eps"]
+        c.theta_sliding = tc["rope_parameters"]["sliding_attention"]["rope_theta"]
+        c.theta_full = tc["rope_parameters"]["full_attention"]["rope_theta"]
+        c.max_positions = max_positions or tc.get("max_position_embeddings", 8192)
+        c.dtype, c.attn_flags = _dtype_code(self.dtype), attn_flags
+        tops = ["ple.per_layer_model_projection.weight", "ple.per_layer_projection_norm.weight", "norm.weight",
+                "embedding_projection.weight"]
+        self._keep = [t0] + [weights[n].contiguous() for n in tops]
+        over = tc.get("per_layer_config", {})
+        layers = (Gemma2LayerWeights * c.layers)()
+        for i in range(c.layers):
+            p = f"layers.{i}."
+            W = lambda n: weights[p + n].contiguous()
+            o = over.get(f"{i:02d}", {})
+            layers[i].full = 1 if tc["layer_types"][i] == "full_attention" else 0
+            layers[i].head_dim = o.get("head_dim", 0)
+            layers[i].kv_heads = o.get("num_key_value_heads", 0)
+            qkv = torch.cat([W("self_attn.q_proj.weight"), W("self_attn.k_proj.weight"),
+                             W("self_attn.v_proj.weight")], 0).contiguous()
+            gu = torch.cat([W("mlp.gate_proj.weight"), W("mlp.up_proj.weight")], 0).contiguous()
+            parts = [qkv, W("self_attn.o_proj.weight"), gu, W("mlp.down_proj.weight"), W("self_attn.q_norm.weight"),
+                     W("self_attn.k_norm.weight"), W("input_layernorm.weight"), W("post_attention_layernorm.weight"),
+                     W("pre_feedforward_layernorm.weight"), W("post_feedforward_layernorm.weight"),
+                     W("ple_block.per_layer_input_gate.weight"), W("ple_block.per_layer_projection.weight"),
+                     W("ple_block.post_per_layer_input_norm.weight"), W("layer_scalar")]
+            for t in parts:
+                if t.dtype != self.dtype or not t.is_cuda:
+                    raise InlError(-1, f"layer {i}: every weight must be a {self.dtype} device tensor")
+            self._keep += parts
+            for name, t in zip(_G2_WEIGHTS, parts):
+                setattr(layers[i], name, t.data_ptr())
+        h = c_void_p()
+        _check(_g2_create(ctypes.byref(c), t0.data_ptr(), layers, *[t.data_ptr() for t in self._keep[1:5]],
+                          ctypes.byref(h)))
+        self._h = h
+
+    def workspace_bytes(self, cu_seqlens) -> int:
+        cu = _cu_array(cu_seqlens)
+        n = ctypes.c_size_t()
+        _check(_g2_ws(self._h, len(cu_seqlens) - 1, cu, ctypes.byref(n)))
+        return n.value
+
+    def encode(self, ids, cu_seqlens, *, out_dim=None, out=None, workspace=None, stream=None):
+        """``ids``: host int sequence of the packed token ids; returns f32
+        ``[texts, out_dim]`` unit vectors on the device (``out_dim`` below
+        ``embedding_dim``: Matryoshka truncation, renormalised)."""
+        import numpy as np
+        import torch
+        cu = _cu_array(cu_seqlens)
+        nt = len(cu_seqlens) - 1
+        od = int(out_dim or self.embedding_dim)
+        idv = np.ascontiguousarray(ids, dtype=np.int32)
+        if len(idv) != int(cu_seqlens[-1]):
+            raise InlError(-1, f"encode: {len(idv)} ids for {int(cu_seqlens[-1])} tokens")
+        dev = self._keep[0].device
+        if out is None:
+            out = torch.empty((nt, od), dtype=torch.float32, device=dev)
+        need = self.workspace_bytes(cu_seqlens)
+        if workspace is None:
+            workspace = getattr(self, "_last_ws", None)
+        if workspace is None or workspace.numel() < need + 256:
+            workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+        ptr = workspace.data_ptr()
+        ptr += (-ptr) % 256
+        _check(_g2_encode(self._h, nt, cu, idv.ctypes.data, od, out.data_ptr(), ptr, need, _stream_ptr(stream)))
+        self._last_ws = workspace
+        return out
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _check(_g2_destroy(self._h))
+            self._h = c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 _sd_ws = _sig("inl_splade_decoder_workspace_size", ctypes.c_int, c_i32, c_i32, ctypes.POINTER(ctypes.c_size_t))
 _sd_max = _sig("inl_splade_decoder_max_fwd", ctypes.c_int, c_i32, c_void_p, c_void_p, c_i64, c_i32, c_void_p, c_i64,
                c_i32, c_i32, c_void_p, c_void_p, ctypes.c_size_t, c_void_p)

@@ -171,6 +171,87 @@ int inl_qwen3_set_graphs(inl_qwen3* enc, int32_t enable);
  * that shape. */
 int inl_qwen3_graph_info(inl_qwen3* enc, int32_t* enabled, int32_t* held);
 
+/* ------------------------------------------------------------------------
+ * EmbeddingGemma 2 text-tower runner: the GPU counterpart of
+ * Gemma2Model::forward_pooled (crates/inl-text/src/gemma2.rs:612-662, the
+ * layer of :473-494, the attention of :381-441, the MLP of :249-254 and the
+ * per-layer-input block of :279-283) over packed texts: bidirectional
+ * attention, sliding layers windowed to |q - k| <= sliding_window, mean
+ * pooling, the embedding projection and L2, then optionally the Matryoshka
+ * truncate-and-renormalise of crates/inl-text/src/native.rs:822-830.
+ * As for Qwen3 the weights stay the caller's, in `dtype`, with
+ *   qkv_proj:     [(heads + 2 kv_heads) * head_dim, hidden] = q, k, v rows;
+ *   gate_up_proj: [2 * intermediate, hidden] = gate rows, then up rows.
+ * The residual stream is f32; GEMM inputs and attention run in `dtype`.
+ * --------------------------------------------------------------------- */
+typedef struct inl_gemma2_config {
+  int32_t vocab;
+  int32_t hidden;
+  int32_t intermediate;
+  int32_t layers;
+  int32_t heads;
+  int32_t kv_heads;        /* default; a layer may override it */
+  int32_t head_dim;        /* default; a layer may override it */
+  int32_t ple_dim;         /* hidden_size_per_layer_input */
+  int32_t embedding_dim;   /* rows of embedding_projection */
+  int32_t sliding_window;  /* inclusive radius of the sliding layers */
+  float eps;               /* rms_norm_eps */
+  double theta_sliding;    /* rope_theta of sliding_attention layers */
+  double theta_full;       /* rope_theta of full_attention layers */
+  int32_t max_positions;   /* longest text the RoPE tables cover */
+  int32_t dtype;           /* enum inl_dtype of the weights and activations */
+  int32_t attn_flags;      /* INL_ATTN_* */
+} inl_gemma2_config;
+
+typedef struct inl_gemma2_layer_weights {
+  int32_t full;            /* 1 = full_attention, 0 = sliding_attention */
+  int32_t head_dim;        /* 0 = the config's (per_layer_config override) */
+  int32_t kv_heads;        /* 0 = the config's */
+  const void* qkv_proj;
+  const void* o_proj;      /* [hidden, heads * head_dim] */
+  const void* gate_up_proj;
+  const void* down_proj;   /* [hidden, intermediate] */
+  const void* q_norm;      /* [head_dim] */
+  const void* k_norm;      /* [head_dim] */
+  const void* input_norm;              /* [hidden] */
+  const void* post_attention_norm;     /* [hidden] */
+  const void* pre_feedforward_norm;    /* [hidden] */
+  const void* post_feedforward_norm;   /* [hidden] */
+  const void* ple_input_gate;          /* [ple_dim, hidden] */
+  const void* ple_projection;          /* [hidden, ple_dim] */
+  const void* ple_post_norm;           /* [hidden] */
+  const void* layer_scalar;            /* [1] */
+} inl_gemma2_layer_weights;
+
+typedef struct inl_gemma2 inl_gemma2;
+
+/* Keeps the weight pointers; builds the two RoPE tables (f64 angles,
+ * gemma2.rs:292-315) and f32 copies of the layer scalars on the current
+ * device - the only allocations the runner makes. ple_model_projection:
+ * [layers * ple_dim, hidden]; ple_norm: [ple_dim]; final_norm: [hidden];
+ * embedding_projection: [embedding_dim, hidden]. */
+int inl_gemma2_create(const inl_gemma2_config* cfg, const void* embed_tokens,
+                      const inl_gemma2_layer_weights* layers,
+                      const void* ple_model_projection, const void* ple_norm,
+                      const void* final_norm, const void* embedding_projection,
+                      inl_gemma2** enc);
+int inl_gemma2_destroy(inl_gemma2* enc);
+
+/* Device workspace one encode of these texts needs. */
+int inl_gemma2_workspace_size(const inl_gemma2* enc, int32_t n_texts,
+                              const int32_t* cu_seqlens_host, size_t* bytes);
+
+/* embeddings (device f32 [n_texts, out_dim]) = the L2-normalised projection
+ * of each text's mean final hidden state (1e-12 inside the square root,
+ * gemma2.rs:660-661); out_dim < embedding_dim keeps the first out_dim
+ * values and normalises them again (Matryoshka; a zero row stays zero).
+ * ids_host: [cu_seqlens_host[n_texts]] token ids, checked against vocab.
+ * Texts of length 0 are refused. Launches run eagerly on `stream`. */
+int inl_gemma2_encode(inl_gemma2* enc, int32_t n_texts,
+                      const int32_t* cu_seqlens_host, const int32_t* ids_host,
+                      int32_t out_dim, float* embeddings, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,152 @@
+"""GPU end-to-end EmbeddingGemma 2 encode (inl_gemma2_* through the C ABI).
+
+- The reference's tiny checkpoint (tests/golden/tiny_embeddinggemma2: 6
+  layers, sliding radius 3, full layers with head_dim 32 and one KV head by
+  per_layer_config) against the golden vectors HF transformers produced for
+  it (gemma2.rs:942-967): every text batched and alone, at max_length 64 and
+  9, within the reference's own 2e-5 (f32).
+- Matryoshka: out_dim below embedding_dim equals the renormalised prefix of
+  the full embedding (native.rs:822-830).
+- The configuration-3 shape (hidden 768, 3 Q / 1 KV heads x 256, radius
+  512, intermediate 1152, per-layer input 256) with seeded random weights,
+  6 layers (layer 5 full), texts longer than the window, against
+  oracle/gemma2.py in f64: f32 within cosine 0.99999 and 5e-4 max-abs (six
+  768-wide layers of f32 GEMM rounding); bf16
+  (weights rounded to bf16, the oracle on those same weights) cosine >= 0.999.
+- All 24 layers of that shape in f32: cosine >= 0.9999.
+- The runner refuses ids outside the vocabulary, empty texts and a bad
+  out_dim on the host.
+"""
+import numpy as np
+import pytest
+
+import tiny_encoders as te
+from oracle import attention as oa
+from oracle import gemma2 as og
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-5   # gemma2.rs:953,963
+
+
+def _device_weights(W, torch, dev, dtype, prefix=""):
+    return {k[len(prefix):]: torch.from_numpy(np.ascontiguousarray(v, dtype=np.float32)).to(dev).to(dtype)
+            for k, v in W.items() if k.startswith(prefix)}
+
+
+def _cosines(a, b):
+    a = a / np.linalg.norm(a, axis=1, keepdims=True)
+    b = b / np.linalg.norm(b, axis=1, keepdims=True)
+    return (a * b).sum(1)
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    return te.load_fixture("tiny_embeddinggemma2")
+
+
+def test_tiny_runner_matches_golden(tiny, cuda, inl):
+    import torch
+    cfg, W, golden, fdir = tiny
+    enc = inl.Gemma2Encoder(cfg["text_config"], _device_weights(W, torch, cuda, torch.float32, "language_model."),
+                            max_positions=64)
+    worst = 0.0
+    for case in golden["cases"]:
+        ids = te.tokenize(fdir, golden["texts"], case["max_length"])
+        lens = [len(x) for x in ids]
+        assert lens == case["lengths"]
+        cu = oa.cu_from_lengths(lens).tolist()
+        print(f"case=gemma2_tiny max_length={case['max_length']} lengths={lens}", flush=True)
+        got = enc.encode(np.concatenate(ids), cu).cpu().numpy()
+        err = np.abs(got - np.asarray(case["batched"])).max()
+        assert err < TOL, f"max_length {case['max_length']} batched: {err:.3g}"
+        worst = max(worst, err)
+        for i, row in enumerate(ids):
+            alone = enc.encode(row, [0, len(row)]).cpu().numpy()
+            err = np.abs(alone[0] - np.asarray(case["alone"][i])).max()
+            assert err < TOL, f"max_length {case['max_length']} alone row {i}: {err:.3g}"
+            worst = max(worst, err)
+    enc.close()
+    print(f"tiny EmbeddingGemma2 runner: worst max-abs {worst:.3g}", flush=True)
+
+
+def test_matryoshka_prefix_is_renormalised(tiny, cuda, inl):
+    import torch
+    cfg, W, golden, fdir = tiny
+    enc = inl.Gemma2Encoder(cfg["text_config"], _device_weights(W, torch, cuda, torch.float32, "language_model."),
+                            max_positions=64)
+    ids = te.tokenize(fdir, golden["texts"], 64)
+    cu = oa.cu_from_lengths([len(x) for x in ids]).tolist()
+    flat = np.concatenate(ids)
+    full = enc.encode(flat, cu).cpu().numpy().astype(np.float64)
+    for d in (8, 16):
+        got = enc.encode(flat, cu, out_dim=d).cpu().numpy()
+        want = full[:, :d] / np.linalg.norm(full[:, :d], axis=1, keepdims=True)
+        assert got.shape == (len(ids), d)
+        assert np.abs(got - want).max() < 1e-6, d
+    enc.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_config3_shape_six_layers(dtype, cuda, inl):
+    import torch
+    from inl_hip import workloads as wl
+    tc = wl.gemma2_config3(vocab=4096, layers=6)
+    W = wl.gemma2_random_weights(tc, seed=7)
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    wd = _device_weights(W, torch, cuda, td)
+    if dtype == "bf16":   # the oracle runs on the bf16-rounded weights
+        W = {k: v.float().cpu().numpy() for k, v in wd.items()}
+    lengths = [700, 64, 513, 1, 130]
+    ids = np.random.default_rng(3).integers(0, tc["vocab_size"], sum(lengths))
+    cu = oa.cu_from_lengths(lengths)
+    print(f"case=gemma2_config3_6layer {dtype} lengths={lengths}", flush=True)
+    enc = inl.Gemma2Encoder(tc, wd, max_positions=1024)
+    got = enc.encode(ids, cu.tolist()).cpu().numpy().astype(np.float64)
+    enc.close()
+    ref = og.encode(W, tc, ids, cu)
+    cos = _cosines(got, ref)
+    err = np.abs(got - ref).max()
+    print(f"gemma2_config3_6layer {dtype}: min cosine {cos.min():.8f}, max abs {err:.3g}", flush=True)
+    assert np.allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
+    if dtype == "f32":
+        assert cos.min() >= 0.99999 and err <= 5e-4
+    else:
+        assert cos.min() >= 0.999
+
+
+def test_config3_shape_full_depth_f32(cuda, inl):
+    """All 24 layers (four of them full) at the configuration-3 width, f32:
+    cosine >= 0.9999 against the oracle in f64 (the north star's
+    pooled-embedding bound)."""
+    import torch
+    from inl_hip import workloads as wl
+    tc = wl.gemma2_config3(vocab=4096)
+    W = wl.gemma2_random_weights(tc, seed=8)
+    lengths = [700, 64, 513, 1, 130]
+    ids = np.random.default_rng(4).integers(0, tc["vocab_size"], sum(lengths))
+    cu = oa.cu_from_lengths(lengths)
+    print(f"case=gemma2_config3_24layer f32 lengths={lengths}", flush=True)
+    enc = inl.Gemma2Encoder(tc, _device_weights(W, torch, cuda, torch.float32), max_positions=1024)
+    got = enc.encode(ids, cu.tolist()).cpu().numpy().astype(np.float64)
+    enc.close()
+    cos = _cosines(got, og.encode(W, tc, ids, cu))
+    print(f"gemma2_config3_24layer f32: min cosine {cos.min():.8f}", flush=True)
+    assert cos.min() >= 0.9999
+
+
+def test_runner_refuses_bad_inputs(tiny, cuda, inl):
+    import torch
+    cfg, W, _, _ = tiny
+    enc = inl.Gemma2Encoder(cfg["text_config"], _device_weights(W, torch, cuda, torch.float32, "language_model."),
+                            max_positions=64)
+    vocab = cfg["text_config"]["vocab_size"]
+    with pytest.raises(inl.InlError, match="outside the vocabulary"):
+        enc.encode([1, vocab, 2], [0, 3])
+    with pytest.raises(inl.InlError, match="empty"):
+        enc.encode([1, 2], [0, 0, 2])
+    with pytest.raises(inl.InlError, match="out_dim"):
+        enc.encode([1, 2], [0, 2], out_dim=cfg["text_config"]["embedding_dim"] + 1)
+    with pytest.raises(inl.InlError, match="max_positions"):
+        enc.encode([1] * 65, [0, 65])
+    enc.close()

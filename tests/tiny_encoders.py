@@ -20,6 +20,7 @@ import numpy as np
 
 from oracle import attention as oa
 from oracle import gdn as ogdn
+from oracle import gemma2 as og
 from oracle import pooling as opool
 from oracle import prologue as opro
 
@@ -166,68 +167,17 @@ def _positions(lens):
 # ---------------------------------------------------------------------------
 
 def gemma2_embed(fixture, texts, max_length: int, ops):
-    """Unit-length embeddings ``[B, embedding_dim]``, following
-    gemma2.rs:606-662 (embedding scale, per-layer inputs, layers, final norm,
-    mean over real tokens, projection, L2) with the layer of :473-496, the
-    attention of :381-441 (per-head q/k RMSNorm + RoPE, weightless v norm,
-    scale 1, sliding layers masked to ``|q - k| <= sliding_window``) and the
-    per-layer-input block of :279-283. Rows are packed; the reference right
-    pads them and masks the padding, which is the same function for the real
-    rows."""
+    """Unit-length embeddings ``[B, embedding_dim]`` of the fixture's tokens
+    for ``texts`` (and their lengths): ``oracle.gemma2.encode`` (the forward
+    of gemma2.rs:606-662 over packed rows) with the hot-path ops routed to
+    ``ops``. The reference right pads the rows and masks the padding, which
+    is the same function for the real rows."""
     cfg, W, _, fdir = fixture
-    tc = cfg["text_config"]
     ids = tokenize(fdir, texts, max_length)
     lens = [len(x) for x in ids]
     cu = oa.cu_from_lengths(lens)
     flat = np.concatenate([np.asarray(x, dtype=np.int64) for x in ids])
-    pos = _positions(lens)
-    hs, eps = tc["hidden_size"], tc["rms_norm_eps"]
-    n_layers, ple_dim = tc["num_hidden_layers"], tc["hidden_size_per_layer_input"]
-    p = "language_model."
-
-    def lin(x, name):
-        return x @ W[p + name + ".weight"].T
-
-    def layer_shape(i):
-        over = tc.get("per_layer_config", {}).get(f"{i:02d}", {})
-        return (tc["layer_types"][i], over.get("head_dim", tc["head_dim"]),
-                over.get("num_key_value_heads", tc["num_key_value_heads"]))
-
-    positions = max(lens) if lens else 1
-    tables = {}
-    for kind, key in (("sliding_attention", "sliding_attention"), ("full_attention", "full_attention")):
-        hd = next((layer_shape(i)[1] for i in range(n_layers) if layer_shape(i)[0] == kind), tc["head_dim"])
-        tables[kind] = opro.rope_table(hd, tc["rope_parameters"][key]["rope_theta"], positions)
-
-    h = W[p + "embed_tokens.weight"][flat] * np.sqrt(float(hs))
-    per_layer = (lin(h, "ple.per_layer_model_projection") * hs ** -0.5).reshape(-1, n_layers, ple_dim)
-    per_layer = opro.rms_norm(per_layer, W[p + "ple.per_layer_projection_norm.weight"], eps)
-    heads = tc["num_attention_heads"]
-    n = h.shape[0]
-    for i in range(n_layers):
-        kind, hd, kvh = layer_shape(i)
-        lp = f"layers.{i}."
-        x = opro.rms_norm(h, W[p + lp + "input_layernorm.weight"], eps)
-        q = lin(x, lp + "self_attn.q_proj").reshape(n, heads, hd)
-        k = lin(x, lp + "self_attn.k_proj").reshape(n, kvh, hd)
-        v = lin(x, lp + "self_attn.v_proj").reshape(n, kvh, hd)
-        q = ops.norm_rope(q, W[p + lp + "self_attn.q_norm.weight"], eps, tables[kind], pos)
-        k = ops.norm_rope(k, W[p + lp + "self_attn.k_norm.weight"], eps, tables[kind], pos)
-        v = ops.norm_rope(v, None, eps)
-        window = tc["sliding_window"] if kind == "sliding_attention" else -1
-        a = ops.attention(q, k, v, cu, causal=False, window=window, scale=1.0)
-        a = lin(a.reshape(n, heads * hd), lp + "self_attn.o_proj")
-        h = h + opro.rms_norm(a, W[p + lp + "post_attention_layernorm.weight"], eps)
-        m = opro.rms_norm(h, W[p + lp + "pre_feedforward_layernorm.weight"], eps)
-        m = lin(gelu_tanh(lin(m, lp + "mlp.gate_proj")) * lin(m, lp + "mlp.up_proj"), lp + "mlp.down_proj")
-        h = h + opro.rms_norm(m, W[p + lp + "post_feedforward_layernorm.weight"], eps)
-        g = gelu_tanh(lin(h, lp + "ple_block.per_layer_input_gate")) * per_layer[:, i, :]
-        h = h + opro.rms_norm(lin(g, lp + "ple_block.per_layer_projection"),
-                              W[p + lp + "ple_block.post_per_layer_input_norm.weight"], eps)
-        h = h * W[p + lp + "layer_scalar"][0]
-    h = opro.rms_norm(h, W[p + "norm.weight"], eps)
-    pooled = ops.mean_pool(h, cu)
-    return ops.l2(lin(pooled, "embedding_projection")), lens
+    return og.encode(W, cfg["text_config"], flat, cu, ops=ops, prefix="language_model."), lens
 
 
 # ---------------------------------------------------------------------------
