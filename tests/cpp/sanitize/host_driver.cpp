@@ -163,6 +163,40 @@ void sizers_and_refusals() {
                                 nullptr) < 0, "gated norm refuses dv 129");
   expect(inl_pool_last_fwd(-1, nullptr, 8, 0, INL_F32, nullptr, nullptr, 1e-6f, 0, nullptr, nullptr) < 0,
          "pool_last refuses n < 0");
+  // EmbeddingGemma 2 runner: every refusal below happens before any device call
+  inl_gemma2* g = nullptr;
+  expect(inl_gemma2_create(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &g) < 0 && !g,
+         "gemma2 refuses a NULL config");
+  inl_gemma2_config gc{};
+  gc.vocab = 64; gc.hidden = 32; gc.intermediate = 64; gc.layers = 2; gc.heads = 4; gc.kv_heads = 2;
+  gc.head_dim = 16; gc.ple_dim = 16; gc.embedding_dim = 24; gc.sliding_window = 3; gc.eps = 1e-6f;
+  gc.theta_sliding = 1e4; gc.theta_full = 1e6; gc.max_positions = 64; gc.dtype = INL_F32;
+  expect(inl_gemma2_create(&gc, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &g) < 0 && !g,
+         "gemma2 refuses NULL weights");
+  gc.hidden = 30;
+  expect(inl_gemma2_create(&gc, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &g) < 0 && !g,
+         "gemma2 refuses hidden % 8");
+  gc.hidden = 32;
+  gc.kv_heads = 3;
+  const char dummy[16] = {};
+  std::vector<inl_gemma2_layer_weights> lw(2);
+  for (auto& l : lw) {
+    const void* d = dummy;
+    l.qkv_proj = l.o_proj = l.gate_up_proj = l.down_proj = l.q_norm = l.k_norm = l.input_norm = d;
+    l.post_attention_norm = l.pre_feedforward_norm = l.post_feedforward_norm = l.ple_input_gate = d;
+    l.ple_projection = l.ple_post_norm = l.layer_scalar = d;
+  }
+  expect(inl_gemma2_create(&gc, dummy, lw.data(), dummy, dummy, dummy, dummy, &g) < 0 && !g,
+         "gemma2 refuses KV heads that do not divide the heads");
+  gc.kv_heads = 2;
+  lw[1].head_dim = 24;
+  expect(inl_gemma2_create(&gc, dummy, lw.data(), dummy, dummy, dummy, dummy, &g) < 0 && !g,
+         "gemma2 refuses a head_dim override that is not 8 x a power of two");
+  size_t gb = 0;
+  expect(inl_gemma2_workspace_size(nullptr, 1, nullptr, &gb) < 0, "gemma2 workspace refuses NULL");
+  expect(inl_gemma2_encode(nullptr, 1, nullptr, nullptr, 1, nullptr, nullptr, 0, nullptr) < 0,
+         "gemma2 encode refuses NULL");
+  expect(inl_gemma2_destroy(nullptr) == INL_OK, "gemma2 destroy of NULL");
 }
 
 }  // namespace
