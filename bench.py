@@ -412,8 +412,8 @@ def op_workload(name, torch, inl_hip, dev):
     """The prologue and epilogue kernels at their configurations' full sizes.
     Returns (label, kernel, launches per step, step(evs), tokens per step,
     algorithmic HBM bytes per step, dtype). Bytes are what the op must move:
-    its inputs read once and its outputs written once (SURVEY-style per-unit
-    figures, stated in each label)."""
+    its inputs read once and its outputs written once (per-unit figures,
+    stated in each label)."""
     from inl_hip import workloads as w
     g = torch.Generator(device=dev).manual_seed(3)
     stream = torch.cuda.current_stream()
@@ -642,7 +642,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards by independent texts, see DESIGN.md", file=sys.stderr)
+              "the path shards by independent texts (one GPU's texts per rank)", file=sys.stderr)
         sys.exit(2)
 
     if args.workload in OP_WORKLOADS:
