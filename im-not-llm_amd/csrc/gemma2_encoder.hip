@@ -337,13 +337,16 @@ extern "C" int inl_gemma2_create(const inl_gemma2_config* cfg, const void* embed
   e->emb_proj = embedding_projection;
   e->layers.assign(layers, layers + cfg->layers);
   // one table per layer kind, at the head_dim of the first layer of that kind (gemma2.rs:566-573)
-  for (int kind = 0; kind < 2; ++kind) {
-    e->hd_kind[kind] = cfg->head_dim;
-    for (int i = 0; i < cfg->layers; ++i)
-      if ((layers[i].full ? 1 : 0) == kind) {
-        e->hd_kind[kind] = layers[i].head_dim > 0 ? layers[i].head_dim : cfg->head_dim;
-        break;
-      }
+  for (int kind = 0; kind < 2 && !rc; ++kind) {
+    e->hd_kind[kind] = -1;
+    for (int i = 0; i < cfg->layers; ++i) {
+      if ((layers[i].full ? 1 : 0) != kind) continue;
+      const int hd = layers[i].head_dim > 0 ? layers[i].head_dim : cfg->head_dim;
+      if (e->hd_kind[kind] < 0) e->hd_kind[kind] = hd;
+      else if (hd != e->hd_kind[kind])   // the kind's one RoPE table must fit every layer of it
+        rc = fail(INL_E_UNSUPPORTED, "gemma2: layers of one kind must share a head_dim (one RoPE table per kind)");
+    }
+    if (e->hd_kind[kind] < 0) e->hd_kind[kind] = cfg->head_dim;
   }
   for (int kind = 0; kind < 2 && !rc; ++kind) {
     const int half = e->hd_kind[kind] / 2;

@@ -192,6 +192,9 @@ void sizers_and_refusals() {
   lw[1].head_dim = 24;
   expect(inl_gemma2_create(&gc, dummy, lw.data(), dummy, dummy, dummy, dummy, &g) < 0 && !g,
          "gemma2 refuses a head_dim override that is not 8 x a power of two");
+  lw[1].head_dim = 32;   // both layers sliding: 16 and 32 cannot share the kind's one RoPE table
+  expect(inl_gemma2_create(&gc, dummy, lw.data(), dummy, dummy, dummy, dummy, &g) < 0 && !g,
+         "gemma2 refuses two head dims within one layer kind");
   size_t gb = 0;
   expect(inl_gemma2_workspace_size(nullptr, 1, nullptr, &gb) < 0, "gemma2 workspace refuses NULL");
   expect(inl_gemma2_encode(nullptr, 1, nullptr, nullptr, 1, nullptr, nullptr, 0, nullptr) < 0,
