@@ -62,13 +62,13 @@ class Ops:
         return y
 
     def attention(self, q, k, v, cu, *, causal, window, scale):
-        return oa.varlen_attention(q, k, v, cu, causal=causal, window=window, scale=scale)
+        return oa.varlen_attention(q, k, v, cu, causal=causal, window=window, scale=scale, dtype=self.dtype)
 
     def mean_pool(self, h, cu):
-        return opool.mean_pool(h, cu)
+        return opool.mean_pool(h, cu, dtype=self.dtype)
 
     def l2(self, x):
-        return opool.l2_normalize(x)
+        return opool.l2_normalize(x, dtype=self.dtype)
 
 
 def encode(W, tc, ids, cu, ops=None, prefix="", dtype=np.float64):

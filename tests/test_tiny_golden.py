@@ -45,6 +45,23 @@ def test_gemma2_tiny_oracle_matches_golden(gemma2):
     print(f"tiny EmbeddingGemma2 oracle: worst max-abs {worst:.3g}")
 
 
+def test_gemma2_tiny_oracle_f32_mode_matches_golden(gemma2):
+    """oracle.gemma2.encode in f32 arithmetic (the CPU baseline's mode) on the
+    golden texts: within 1e-5 of the golden vectors (f32 rounding of six
+    32-wide layers; the f64 mode is held to the reference's 2e-5 above)."""
+    from oracle import attention as oa
+    from oracle import gemma2 as og
+    cfg, W, golden, fdir = gemma2
+    case = golden["cases"][0]
+    ids = te.tokenize(fdir, golden["texts"], case["max_length"])
+    cu = oa.cu_from_lengths([len(x) for x in ids])
+    emb = og.encode(W, cfg["text_config"], np.concatenate(ids), cu, prefix="language_model.", dtype=np.float32)
+    assert emb.dtype == np.float32
+    err = np.abs(emb - np.asarray(case["batched"])).max()
+    print(f"tiny EmbeddingGemma2 oracle f32: max-abs {err:.3g}")
+    assert err < 1e-5, err
+
+
 class _Planted(te.OracleOps):
     """The oracle with one plausible mistake in the attention mask."""
 
