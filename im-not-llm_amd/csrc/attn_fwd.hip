@@ -564,21 +564,24 @@ int unit_weight(const KernelCfg& cfg, const inl_attn_desc* d, int T, int q0, int
   if (!cfg.persistent) return 8 * tiles + 18;
   const int BN = cfg.bn;
   const int rows = std::min(T, q0 + BM) - q0;
-  int masked = 0;
-  for (int t = lo_t; t < hi_t; ++t) {
-    bool need = false;
-    for (int r0 = q0; r0 < q0 + BM && !need; r0 += 32) {
-      if (r0 >= T) { need = true; break; }
-      const int rlast = std::min(r0 + 31, T - 1);
-      int e = T;
-      if (d->causal) e = std::min(e, r0 + 1);
-      if (d->window >= 0) e = std::min(e, r0 + d->window + 1);
-      const int f_hi = e / BN;
-      const int f_lo = d->window >= 0 ? (std::max(0, rlast - d->window) + BN - 1) / BN : 0;
-      need = t < f_lo || t >= f_hi;
+  // Tiles on which some 32-row chunk of the unit needs a mask: those outside
+  // the intersection of the chunks' unmasked tile ranges [f_lo, f_hi) (the
+  // kernel's per-wave test); all of them when a chunk lies past the text.
+  int a = lo_t, b = hi_t;
+  bool all = false;
+  for (int r0 = q0; r0 < q0 + BM && !all; r0 += 32) {
+    if (r0 >= T) {
+      all = true;
+      break;
     }
-    masked += need;
+    const int rlast = std::min(r0 + 31, T - 1);
+    int e = T;
+    if (d->causal) e = std::min(e, r0 + 1);
+    if (d->window >= 0) e = std::min(e, r0 + d->window + 1);
+    a = std::max(a, d->window >= 0 ? (std::max(0, rlast - d->window) + BN - 1) / BN : 0);
+    b = std::min(b, e / BN);
   }
+  const int masked = all ? tiles : tiles - std::max(0, b - a);
   if (cfg.d == 256) return 8 * tiles + 46 + masked + (rows * 7 + 32) / 64;
   return 8 * tiles + 17 + 3 * masked + (rows * 35 + 512) / 1024;
 }
