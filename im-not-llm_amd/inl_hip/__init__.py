@@ -182,6 +182,23 @@ def _dtype_code(t) -> int:
     raise InlError(-1, f"unsupported dtype {t}")
 
 
+def _weight(weights, name, shape, dtype):
+    """``weights[name]`` as a contiguous device tensor, after checking its
+    dtype and shape: the runners take bare pointers and size every read from
+    the configuration, so a tensor of another shape would be read past its
+    end."""
+    t = weights.get(name)
+    if t is None:
+        raise InlError(-1, f"weight {name} is missing")
+    if t.dtype != dtype:
+        raise InlError(-1, f"weight {name}: dtype {t.dtype}, the runner's is {dtype}")
+    if tuple(t.shape) != tuple(int(s) for s in shape):
+        raise InlError(-1, f"weight {name}: shape {tuple(t.shape)}, the configuration needs {tuple(shape)}")
+    if not t.is_cuda:
+        raise InlError(-1, f"weight {name}: not a device tensor ({t.device})")
+    return t.contiguous()
+
+
 def _stream_ptr(stream) -> int:
     import torch
     if stream is None:
@@ -607,25 +624,25 @@ class Qwen3Encoder:
         c.heads, c.kv_heads, c.head_dim = cfg.heads, cfg.kv_heads, cfg.head_dim
         c.eps, c.rope_theta, c.max_positions = cfg.eps, cfg.theta, max_positions
         c.dtype, c.attn_flags = _dtype_code(self.dtype), attn_flags
-        self._keep = [t0, weights["norm.weight"]]
+        dt, hs, ff = self.dtype, cfg.hidden, cfg.intermediate
+        qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+        t0 = _weight(weights, "embed_tokens.weight", (cfg.vocab, hs), dt)
+        self._keep = [t0, _weight(weights, "norm.weight", (hs,), dt)]
         layers = (Qwen3LayerWeights * cfg.layers)()
         for i in range(cfg.layers):
             p = f"layers.{i}."
-            W = lambda n: weights[p + n].contiguous()
-            qkv = torch.cat([W("self_attn.q_proj.weight"), W("self_attn.k_proj.weight"),
-                             W("self_attn.v_proj.weight")], 0).contiguous()
-            gu = torch.cat([W("mlp.gate_proj.weight"), W("mlp.up_proj.weight")], 0).contiguous()
-            parts = [qkv, W("self_attn.o_proj.weight"), gu, W("mlp.down_proj.weight"), W("self_attn.q_norm.weight"),
-                     W("self_attn.k_norm.weight"), W("input_layernorm.weight"),
-                     W("post_attention_layernorm.weight")]
-            for t in parts:
-                if t.dtype != self.dtype or not t.is_cuda:
-                    raise InlError(-1, f"layer {i}: every weight must be a {self.dtype} device tensor")
+            W = lambda n, *shape: _weight(weights, p + n, shape, dt)
+            qkv = torch.cat([W("self_attn.q_proj.weight", qd, hs), W("self_attn.k_proj.weight", kvd, hs),
+                             W("self_attn.v_proj.weight", kvd, hs)], 0).contiguous()
+            gu = torch.cat([W("mlp.gate_proj.weight", ff, hs), W("mlp.up_proj.weight", ff, hs)], 0).contiguous()
+            parts = [qkv, W("self_attn.o_proj.weight", hs, qd), gu, W("mlp.down_proj.weight", hs, ff),
+                     W("self_attn.q_norm.weight", cfg.head_dim), W("self_attn.k_norm.weight", cfg.head_dim),
+                     W("input_layernorm.weight", hs), W("post_attention_layernorm.weight", hs)]
             self._keep += parts
             for name, t in zip([f[0] for f in Qwen3LayerWeights._fields_], parts):
                 setattr(layers[i], name, t.data_ptr())
         h = c_void_p()
-        _check(_q3_create(ctypes.byref(c), t0.data_ptr(), layers, weights["norm.weight"].data_ptr(), ctypes.byref(h)))
+        _check(_q3_create(ctypes.byref(c), t0.data_ptr(), layers, self._keep[1].data_ptr(), ctypes.byref(h)))
         self._h = h
 
     def workspace_bytes(self, cu_seqlens) -> int:
@@ -730,29 +747,33 @@ class Gemma2Encoder:
         c.theta_full = tc["rope_parameters"]["full_attention"]["rope_theta"]
         c.max_positions = max_positions or tc.get("max_position_embeddings", 8192)
         c.dtype, c.attn_flags = _dtype_code(self.dtype), attn_flags
-        tops = ["ple.per_layer_model_projection.weight", "ple.per_layer_projection_norm.weight", "norm.weight",
-                "embedding_projection.weight"]
-        self._keep = [t0] + [weights[n].contiguous() for n in tops]
+        dt, hs, ff, ple = self.dtype, c.hidden, c.intermediate, c.ple_dim
+        t0 = _weight(weights, "embed_tokens.weight", (c.vocab, hs), dt)
+        self._keep = [t0, _weight(weights, "ple.per_layer_model_projection.weight", (c.layers * ple, hs), dt),
+                      _weight(weights, "ple.per_layer_projection_norm.weight", (ple,), dt),
+                      _weight(weights, "norm.weight", (hs,), dt),
+                      _weight(weights, "embedding_projection.weight", (c.embedding_dim, hs), dt)]
         over = tc.get("per_layer_config", {})
         layers = (Gemma2LayerWeights * c.layers)()
         for i in range(c.layers):
             p = f"layers.{i}."
-            W = lambda n: weights[p + n].contiguous()
+            W = lambda n, *shape: _weight(weights, p + n, shape, dt)
             o = over.get(f"{i:02d}", {})
             layers[i].full = 1 if tc["layer_types"][i] == "full_attention" else 0
             layers[i].head_dim = o.get("head_dim", 0)
             layers[i].kv_heads = o.get("num_key_value_heads", 0)
-            qkv = torch.cat([W("self_attn.q_proj.weight"), W("self_attn.k_proj.weight"),
-                             W("self_attn.v_proj.weight")], 0).contiguous()
-            gu = torch.cat([W("mlp.gate_proj.weight"), W("mlp.up_proj.weight")], 0).contiguous()
-            parts = [qkv, W("self_attn.o_proj.weight"), gu, W("mlp.down_proj.weight"), W("self_attn.q_norm.weight"),
-                     W("self_attn.k_norm.weight"), W("input_layernorm.weight"), W("post_attention_layernorm.weight"),
-                     W("pre_feedforward_layernorm.weight"), W("post_feedforward_layernorm.weight"),
-                     W("ple_block.per_layer_input_gate.weight"), W("ple_block.per_layer_projection.weight"),
-                     W("ple_block.post_per_layer_input_norm.weight"), W("layer_scalar")]
-            for t in parts:
-                if t.dtype != self.dtype or not t.is_cuda:
-                    raise InlError(-1, f"layer {i}: every weight must be a {self.dtype} device tensor")
+            hd = layers[i].head_dim or c.head_dim
+            qd, kvd = c.heads * hd, (layers[i].kv_heads or c.kv_heads) * hd
+            qkv = torch.cat([W("self_attn.q_proj.weight", qd, hs), W("self_attn.k_proj.weight", kvd, hs),
+                             W("self_attn.v_proj.weight", kvd, hs)], 0).contiguous()
+            gu = torch.cat([W("mlp.gate_proj.weight", ff, hs), W("mlp.up_proj.weight", ff, hs)], 0).contiguous()
+            parts = [qkv, W("self_attn.o_proj.weight", hs, qd), gu, W("mlp.down_proj.weight", hs, ff),
+                     W("self_attn.q_norm.weight", hd), W("self_attn.k_norm.weight", hd),
+                     W("input_layernorm.weight", hs), W("post_attention_layernorm.weight", hs),
+                     W("pre_feedforward_layernorm.weight", hs), W("post_feedforward_layernorm.weight", hs),
+                     W("ple_block.per_layer_input_gate.weight", ple, hs),
+                     W("ple_block.per_layer_projection.weight", hs, ple),
+                     W("ple_block.post_per_layer_input_norm.weight", hs), W("layer_scalar", 1)]
             self._keep += parts
             for name, t in zip(_G2_WEIGHTS, parts):
                 setattr(layers[i], name, t.data_ptr())

@@ -143,6 +143,23 @@ def test_binding_refuses_tensors_the_kernels_would_overrun():
         inl_hip._check_tensors(padded, *good)
 
 
+def test_encoder_weights_are_checked_against_the_configuration():
+    """The encoder runners read every weight at the size the configuration
+    gives, so the binding checks each tensor's dtype and shape before the
+    device (CPU tensors here: the device check comes last)."""
+    import torch
+    import inl_hip
+    w = {"a": torch.zeros(6, 4), "b": torch.zeros(6, 4, dtype=torch.bfloat16)}
+    with pytest.raises(inl_hip.InlError, match="weight c is missing"):
+        inl_hip._weight(w, "c", (6, 4), torch.float32)
+    with pytest.raises(inl_hip.InlError, match="weight b: dtype"):
+        inl_hip._weight(w, "b", (6, 4), torch.float32)
+    with pytest.raises(inl_hip.InlError, match=r"weight a: shape \(6, 4\), the configuration needs \(4, 6\)"):
+        inl_hip._weight(w, "a", (4, 6), torch.float32)
+    with pytest.raises(inl_hip.InlError, match="weight a: not a device tensor"):
+        inl_hip._weight(w, "a", (6, 4), torch.float32)
+
+
 def test_gdn_entry_points_validate_on_the_host():
     """Shapes outside what the gated-delta-net kernels hold are refused
     before any device call (null device pointers are never dereferenced)."""

@@ -15,7 +15,8 @@
   (weights rounded to bf16, the oracle on those same weights) cosine >= 0.999.
 - All 24 layers of that shape in f32: cosine >= 0.9999.
 - The runner refuses ids outside the vocabulary, empty texts and a bad
-  out_dim on the host.
+  out_dim on the host, and weights of another shape, dtype or device when it
+  is built.
 """
 import numpy as np
 import pytest
@@ -150,3 +151,16 @@ def test_runner_refuses_bad_inputs(tiny, cuda, inl):
     with pytest.raises(inl.InlError, match="max_positions"):
         enc.encode([1] * 65, [0, 65])
     enc.close()
+    # weights of another shape, dtype or device are refused before any launch
+    bad = _device_weights(W, torch, cuda, torch.float32, "language_model.")
+    bad["layers.2.self_attn.q_proj.weight"] = bad["layers.1.self_attn.q_proj.weight"]   # a full layer's is wider
+    with pytest.raises(inl.InlError, match="shape"):
+        inl.Gemma2Encoder(cfg["text_config"], bad, max_positions=64)
+    bad = _device_weights(W, torch, cuda, torch.float32, "language_model.")
+    bad["ple.per_layer_model_projection.weight"] = bad["ple.per_layer_model_projection.weight"].cpu()
+    with pytest.raises(inl.InlError, match="not a device tensor"):
+        inl.Gemma2Encoder(cfg["text_config"], bad, max_positions=64)
+    bad = _device_weights(W, torch, cuda, torch.float32, "language_model.")
+    bad["layers.0.layer_scalar"] = bad["layers.0.layer_scalar"].double()
+    with pytest.raises(inl.InlError, match="dtype"):
+        inl.Gemma2Encoder(cfg["text_config"], bad, max_positions=64)

@@ -8,7 +8,8 @@ numpy oracle (oracle/qwen3.py, pinned against transformers' Qwen3Model).
 - Configuration 1 at full size (28 layers, vocab 151,669, 8 texts of
   U[16, 256] tokens = 778 tokens), f32: cosine >= 0.9999 against the oracle
   in f32 (the north star's pooled-embedding bound).
-- The runner refuses ids outside the vocabulary and empty texts on the host.
+- The runner refuses ids outside the vocabulary and empty texts on the host,
+  and weights of another shape, dtype or device when it is built.
 """
 import numpy as np
 import pytest
@@ -92,6 +93,15 @@ def test_runner_refuses_bad_inputs(cuda, inl):
     torch.cuda.synchronize()
     assert np.isfinite(out.cpu().numpy()).all()
     enc.close()
+    # weights of another shape, dtype or device are refused before any launch
+    w = _to_device(oq.random_weights(cfg, seed=5), torch, cuda, torch.float32)
+    w["layers.0.mlp.down_proj.weight"] = w["layers.0.mlp.down_proj.weight"][:, :-8]
+    with pytest.raises(inl.InlError, match="shape"):
+        inl.Qwen3Encoder(cfg, w, max_positions=32)
+    w = _to_device(oq.random_weights(cfg, seed=5), torch, cuda, torch.float32)
+    w["norm.weight"] = w["norm.weight"].cpu()
+    with pytest.raises(inl.InlError, match="not a device tensor"):
+        inl.Qwen3Encoder(cfg, w, max_positions=32)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
