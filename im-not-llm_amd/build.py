@@ -51,22 +51,47 @@ EXTRA = {
 # spill could store that register, or hand it to another value, while the
 # load is still in flight. Their kernels must use no scratch; the build reads
 # the compiler's resource-usage remarks and fails if any of them does.
-NO_SCRATCH = {"attn_pp.hip", "attn_pp64.hip", "attn_wide.hip", "splade_decoder.hip"}
+NO_SCRATCH = {"attn_pp.hip", "attn_pp64.hip", "attn_wide.hip", "gemm.hip", "splade_decoder.hip"}
 RESOURCE_REMARKS = ["-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"]
 
 
 def scratch_users(remarks: str) -> list[str]:
     """Kernels that the compiler's kernel-resource-usage remarks report with
     a nonzero ScratchSize (bytes per lane)."""
-    users, name = [], None
+    return [f"{name} ({size} B/lane)" for name, size in parse_scratch(remarks) if size]
+
+
+def parse_scratch(remarks: str) -> list[tuple[str, int]]:
+    """(function name, ScratchSize) of every function the kernel-resource-usage
+    remarks describe. A function whose remark block has no ScratchSize line
+    is reported with size -1, so that a format change cannot pass silently."""
+    out, name = [], None
     for line in remarks.splitlines():
         if "Function Name:" in line:
+            if name is not None:
+                out.append((name, -1))
             name = line.split("Function Name:", 1)[1].split()[0]
-        elif "ScratchSize [bytes/lane]:" in line:
-            size = int(line.split("ScratchSize [bytes/lane]:", 1)[1].split()[0])
-            if size and name:
-                users.append(f"{name} ({size} B/lane)")
-    return users
+        elif "ScratchSize [bytes/lane]:" in line and name is not None:
+            out.append((name, int(line.split("ScratchSize [bytes/lane]:", 1)[1].split()[0])))
+            name = None
+    if name is not None:
+        out.append((name, -1))
+    return out
+
+
+def check_no_scratch(src_name: str, remarks: str) -> None:
+    """Raise unless the remarks describe at least one kernel, every described
+    function has a ScratchSize, and none of them is nonzero."""
+    parsed = parse_scratch(remarks)
+    if not parsed:
+        raise RuntimeError(f"{src_name}: no kernel-resource-usage remarks were parsed, so the no-scratch "
+                           "check cannot be made")
+    unsized = [n for n, s in parsed if s < 0]
+    if unsized:
+        raise RuntimeError(f"{src_name}: remarks without a ScratchSize for " + ", ".join(unsized))
+    users = scratch_users(remarks)
+    if users:
+        raise RuntimeError(f"{src_name}: kernels with inline-asm loads use scratch: " + ", ".join(users))
 
 
 def sources():
@@ -98,10 +123,7 @@ def build(verbose: bool = False) -> Path:
             if rc != 0:
                 raise RuntimeError(f"hipcc failed on {src.name} ({rc}):\n{err}")
             if src.name in NO_SCRATCH:
-                users = scratch_users(err)
-                if users:
-                    raise RuntimeError(f"{src.name}: kernels with inline-asm loads use scratch: "
-                                       + ", ".join(users))
+                check_no_scratch(src.name, err)
                 err = "\n".join(l for l in err.splitlines() if "kernel-resource-usage" not in l)
             if verbose and err.strip():
                 print(err, file=sys.stderr)

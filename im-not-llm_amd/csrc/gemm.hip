@@ -1,0 +1,342 @@
+// Plain bf16 GEMM on the matrix cores (gfx950): the encoder's projections
+//
+//   y[m, n] = alpha * sum_k x[m, k] * w[n, k]  (+ beta * y[m, n])
+//
+// in the row-major, bias-free Linear convention of the reference
+// (candle_nn::Linear via linear_no_bias, crates/inl-text/src/qwen3/mod.rs:99-104,
+// crates/inl-text/src/gemma2.rs:233-283): x [M, K] rows, w [N, K] rows (the
+// checkpoint's [out, in] layout), y [M, N] rows in f32 or bf16, f32
+// accumulation. No workspace, no allocation, no per-shape tuning, nothing
+// synchronised: a call is one kernel launch, so the same call works under
+// graph capture and for every token count M.
+//
+// Kernel: 256 x 256 output tiles, 8 waves (two per SIMD) as 2 (w rows, i.e.
+// output columns) x 4 (x rows), each wave 128 x 64 = 4 x 2 blocks of
+// v_mfma_f32_32x32x16_bf16 (the w block is the MFMA's row operand, the x
+// block its column operand, so a lane's accumulator holds one output row and
+// four runs of four consecutive output columns: 16-byte f32 stores). The K
+// loop runs through a 3-stage LDS ring of 32-wide k slices (32 KiB a stage),
+// filled by direct global -> LDS loads three stages ahead; each stage's MFMA
+// operands are read into registers one stage ahead. The workgroup is
+// persistent: its tiles form one stream of stages, so the next tile's first
+// loads are in flight while the current tile's epilogue stores run.
+//
+// Tile order: workgroup b runs on XCD b % 8. The tiles, m-tile major (all
+// n-tiles of one 256-row block of x in a row), are cut into 8 contiguous
+// ranges, one per XCD, and each XCD's workgroups take every 32nd tile of its
+// range: the ~32 tiles an XCD runs at one time share their x rows (read from
+// HBM once, then from that XCD's 4 MB L2), and w (at most a few MB) stays in
+// L2 across the range.
+#include <algorithm>
+
+#include "../../include/inl_encoder.h"
+#include "attn_stream.hpp"
+
+namespace inl {
+
+namespace {
+
+constexpr int GM_BM = 256;    // x rows (output rows) per tile
+constexpr int GM_BN = 256;    // w rows (output columns) per tile
+constexpr int GM_BK = 32;     // k per LDS stage (64-byte rows)
+constexpr int GM_STAGES = 3;
+constexpr int GM_ROW = GM_BK * 2;
+constexpr int GM_W = GM_BN * GM_ROW;            // 16 KiB
+constexpr int GM_X = GM_BM * GM_ROW;            // 16 KiB
+constexpr int GM_STAGE = GM_W + GM_X;           // 32 KiB
+constexpr int GM_BLOCKS = GM_STAGE / 1024;      // 1 KiB direct-load blocks per stage
+constexpr int GM_NW = 8;
+constexpr int GM_PER_WAVE = GM_BLOCKS / GM_NW;  // 4
+constexpr int GM_LDS = GM_STAGES * GM_STAGE;    // 96 KiB
+constexpr int GM_XCDS = 8;
+
+static_assert(GM_BLOCKS % GM_NW == 0, "the direct loads split evenly over the waves");
+static_assert(GM_PER_WAVE % 2 == 0, "each wave loads w blocks then x blocks");
+
+struct GemmParams {
+  const char* x;
+  const char* w;
+  char* y;
+  int64_t m;
+  int32_t n, k;
+  int64_t xs_b, ws_b, ys;   // x and w row strides in bytes, y row stride in elements
+  float alpha, beta;
+  int32_t n_tiles_n;        // tiles along n
+  int64_t n_tiles;          // all tiles
+  int64_t per_xcd;          // tiles per XCD range (the last ranges may be short)
+  int32_t wg_per_xcd;       // workgroups per XCD
+};
+
+// 16-byte chunk c (of 4) of tile row r sits at r * 64 + ((c ^ ((r >> 2) & 3)) << 4):
+// the 16 rows one ds_read_b128 pass touches then cover all 64 banks.
+__device__ __forceinline__ uint32_t gm_swz(int r, int c) { return r * GM_ROW + ((c ^ ((r >> 2) & 3)) << 4); }
+
+template <bool OUT_BF16, bool ACC>
+__global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int xcd = blockIdx.x % GM_XCDS;
+  const int slot = blockIdx.x / GM_XCDS;
+  const int64_t first = (int64_t)xcd * p.per_xcd;
+  const int64_t last = min(first + p.per_xcd, p.n_tiles);   // this XCD's range [first, last)
+  const int64_t t0 = first + slot;
+  if (t0 >= last) return;
+  const int my_tiles = (int)((last - 1 - t0) / p.wg_per_xcd + 1);
+  const int kst = p.k / GM_BK;
+  const int total = my_tiles * kst;
+
+  const uint32_t lds0 = lds_addr(smem);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave >> 2, wm = wave & 3;
+  const int l32 = lane & 31, hf = lane >> 5;
+
+  // per-lane offsets of this wave's direct-load blocks inside a tile: blocks
+  // {wave, wave + 8, ...} of the 32 per stage, w rows (blocks 0-15) then x rows
+  uint32_t goff[GM_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < GM_PER_WAVE; ++i) {
+    const int blk = wave + GM_NW * i;
+    const int r = lane >> 2, cp = lane & 3;
+    const int c = cp ^ ((r >> 2) & 3);
+    const bool is_w = i < GM_PER_WAVE / 2;
+    const int row = (is_w ? blk : blk - GM_W / 1024) * 16 + r;
+    goff[i] = (uint32_t)row * (uint32_t)(is_w ? p.ws_b : p.xs_b) + c * 16;
+  }
+  // The descriptors of a tile start at its first x row / w row, so no offset
+  // exceeds 32 bits whatever M is; rows past M or N read as zero.
+  auto tile_of = [&](int j, int64_t* mt, int* nt) __attribute__((always_inline)) {
+    const int64_t t = t0 + (int64_t)j * p.wg_per_xcd;
+    *mt = t / p.n_tiles_n;
+    *nt = (int)(t - *mt * p.n_tiles_n);
+  };
+  auto rsrc_x = [&](int j) __attribute__((always_inline)) {
+    int64_t mt;
+    int nt;
+    tile_of(j, &mt, &nt);
+    const int64_t r0 = mt * GM_BM;
+    const int64_t rows = min((int64_t)GM_BM, p.m - r0);
+    return pp_rsrc_words(p.x + r0 * p.xs_b, (uint32_t)(rows * p.xs_b));
+  };
+  auto rsrc_w = [&](int j) __attribute__((always_inline)) {
+    int64_t mt;
+    int nt;
+    tile_of(j, &mt, &nt);
+    const int r0 = nt * GM_BN;
+    const int rows = min(GM_BN, p.n - r0);
+    return pp_rsrc_words(p.w + (int64_t)r0 * p.ws_b, (uint32_t)((int64_t)rows * p.ws_b));
+  };
+  const i32x4 none = pp_rsrc_words(p.x, 0);   // loads past the last stage read zeros
+
+  // The load cursor (tile ld_j, k stage ld_ks) runs up to three stages ahead
+  // of the MFMA cursor, possibly into the next tile; it carries that tile's
+  // descriptors.
+  int ld_j = 0, ld_ks = 0, ld_slot = 0;
+  i32x4 xrs = rsrc_x(0), wrs = rsrc_w(0);
+  auto issue = [&]() __attribute__((always_inline)) {
+    const uint32_t st = lds0 + (uint32_t)ld_slot * GM_STAGE;
+    const bool live = ld_j < my_tiles;
+    const uint32_t koff = (uint32_t)ld_ks * GM_ROW;
+#pragma unroll
+    for (int i = 0; i < GM_PER_WAVE; ++i) {
+      const int blk = wave + GM_NW * i;
+      const bool is_w = i < GM_PER_WAVE / 2;
+      dma_b128(live ? (is_w ? wrs : xrs) : none, st + blk * 1024, goff[i] + koff);
+    }
+    if (++ld_slot == GM_STAGES) ld_slot = 0;
+    if (++ld_ks == kst) {
+      ld_ks = 0;
+      if (++ld_j < my_tiles) {
+        xrs = rsrc_x(ld_j);
+        wrs = rsrc_w(ld_j);
+      }
+    }
+  };
+
+  // fragment addresses (stage 0): w rows wn*128 + a*32 + l32, x rows wm*64 + b*32 + l32
+  uint32_t fa[4][2], fb[2][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) fa[a][ks] = opaque(lds0 + gm_swz(wn * 128 + a * 32 + l32, 2 * ks + hf));
+#pragma unroll
+    for (int b = 0; b < 2; ++b) fb[b][ks] = opaque(lds0 + GM_W + gm_swz(wm * 64 + b * 32 + l32, 2 * ks + hf));
+  }
+
+  f32x16 acc[4][2];
+  const f32x16 zero = {};
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = zero;
+
+  // MFMA operands of one 16-wide k step: 4 w blocks and 2 x blocks
+  struct Half {
+    u32x4 a[4], b[2];
+  };
+  int rd_slot = 0;   // LDS slot of the stage whose fragments are read next
+  auto read_half = [&](int ks, Half& f) __attribute__((always_inline)) {
+    const uint32_t so = (uint32_t)rd_slot * GM_STAGE;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) f.a[a] = lds_load<u32x4>(fa[a][ks] + so);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) f.b[b] = lds_load<u32x4>(fb[b][ks] + so);
+  };
+  auto mfmas = [&](const Half& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, f.a[a]),
+                                                            __builtin_bit_cast(bf16x8, f.b[b]), acc[a][b], 0, 0, 0);
+  };
+  // tile done: acc[a][b][4 * g + e] is output (row wm*64 + b*32 + l32,
+  // column wn*128 + a*32 + 8*g + 4*hf + e) of the tile
+  int mm_j = 0, mm_ks = 0;   // the MFMA cursor
+  auto tile_end = [&]() __attribute__((always_inline)) {
+    if (++mm_ks != kst) return;
+    mm_ks = 0;
+    int64_t mt;
+    int nt;
+    tile_of(mm_j++, &mt, &nt);
+    const int64_t row0 = mt * GM_BM + wm * 64 + l32;
+    const int col0 = nt * GM_BN + wn * 128 + 4 * hf;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int64_t row = row0 + b * 32;
+      if (row < p.m) {
+        char* yr = p.y + row * p.ys * (OUT_BF16 ? 2 : 4);
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int col = col0 + a * 32 + 8 * g;
+            if (col < p.n) {
+              f32x4 v;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[a][b][4 * g + e];
+              if constexpr (OUT_BF16) {
+                bf16x4* dst = reinterpret_cast<bf16x4*>(yr + (int64_t)col * 2);
+                if constexpr (ACC) {
+                  const bf16x4 o = *dst;
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) v[e] += p.beta * (float)o[e];
+                }
+                bf16x4 r;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r[e] = (bf16)v[e];
+                *dst = r;
+              } else {
+                f32x4* dst = reinterpret_cast<f32x4*>(yr + (int64_t)col * 4);
+                if constexpr (ACC) {
+                  const f32x4 o = *dst;
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) v[e] += p.beta * o[e];
+                }
+                *dst = v;
+              }
+            }
+          }
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) acc[a][b] = zero;
+  };
+  // One iteration per stage s, with h0 holding its first k step's operands:
+  // read its second k step's operands while the first step's MFMAs run;
+  // then wait for stage s + 1 (vmcnt) and for every wave to have read all of
+  // stage s (barrier), refill stage s's LDS slot with stage s + 3, and read
+  // stage s + 1's first k step while the second step's MFMAs run.
+  Half h0, h1;
+  auto step = [&]() __attribute__((always_inline)) {
+    read_half(1, h1);
+    mfmas(h0);
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(GM_PER_WAVE) : "memory");
+    lds_barrier();
+    issue();
+    if (++rd_slot == GM_STAGES) rd_slot = 0;
+    read_half(0, h0);
+    mfmas(h1);
+    tile_end();
+  };
+
+  issue();
+  issue();
+  issue();
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * GM_PER_WAVE) : "memory");   // stage 0
+  lds_barrier();
+  read_half(0, h0);
+  for (int st = 0; st < total; ++st) step();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the dummy loads past the end
+}
+
+template <bool B, bool A>
+const void* gemm_fn() {
+  return (const void*)gemm_bf16_kernel<B, A>;
+}
+
+}  // namespace
+
+}  // namespace inl
+
+extern "C" int inl_gemm_bf16_fwd(int64_t m, int64_t n, int64_t k, const void* x, int64_t x_stride, const void* w,
+                                 int64_t w_stride, int32_t out_dtype, void* y, int64_t y_stride, float alpha,
+                                 float beta, void* stream) {
+  using namespace inl;
+  if (m < 0 || n <= 0 || k <= 0) return fail(INL_E_INVALID, "gemm: m must be >= 0, n and k > 0");
+  if (!dtype_ok(out_dtype)) return fail(INL_E_INVALID, "gemm: out_dtype must be f32 or bf16");
+  if (k % GM_BK || n % 8)
+    return fail(INL_E_UNSUPPORTED, "gemm: k must be a multiple of 32 and n a multiple of 8");
+  if (n > (1 << 30) || k > (1 << 20)) return fail(INL_E_UNSUPPORTED, "gemm: n or k too large");
+  const int64_t xs = x_stride ? x_stride : k, ws = w_stride ? w_stride : k, ys = y_stride ? y_stride : n;
+  if (xs < k || ws < k || ys < n) return fail(INL_E_INVALID, "gemm: a row stride is shorter than its row");
+  if (xs % 8 || ws % 8 || ys % 8) return fail(INL_E_UNSUPPORTED, "gemm: row strides must be multiples of 8 elements");
+  if (m == 0) return INL_OK;
+  if (!x || !w || !y) return fail(INL_E_INVALID, "gemm: NULL x, w or y");
+  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)y & 15))
+    return fail(INL_E_INVALID, "gemm: x, w and y must be 16-byte aligned");
+  // each tile's descriptor spans at most 256 rows of x or w
+  if ((int64_t)GM_BM * xs * 2 >= ((int64_t)1 << 32) || (int64_t)GM_BN * ws * 2 >= ((int64_t)1 << 32))
+    return fail(INL_E_UNSUPPORTED, "gemm: row strides too large for a tile's 32-bit buffer range");
+  int dev = 0, cus = 0;
+  INL_HIP_TRY(hipGetDevice(&dev));
+  INL_HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  GemmParams p{};
+  p.x = (const char*)x;
+  p.w = (const char*)w;
+  p.y = (char*)y;
+  p.m = m;
+  p.n = (int32_t)n;
+  p.k = (int32_t)k;
+  p.xs_b = xs * 2;
+  p.ws_b = ws * 2;
+  p.ys = ys;
+  p.alpha = alpha;
+  p.beta = beta;
+  p.n_tiles_n = (int32_t)((n + GM_BN - 1) / GM_BN);
+  p.n_tiles = ((m + GM_BM - 1) / GM_BM) * p.n_tiles_n;
+  p.per_xcd = (p.n_tiles + GM_XCDS - 1) / GM_XCDS;
+  // one workgroup per CU (96 KiB of LDS each), at most one per tile of an XCD's range
+  const int64_t per_xcd_wg = std::max<int64_t>(1, std::min<int64_t>(cus / GM_XCDS, p.per_xcd));
+  p.wg_per_xcd = (int32_t)per_xcd_wg;
+  if ((int64_t)(p.per_xcd + per_xcd_wg - 1) / per_xcd_wg * (k / GM_BK) >= ((int64_t)1 << 31))
+    return fail(INL_E_UNSUPPORTED, "gemm: too many k stages per workgroup");
+  const bool bf = out_dtype == INL_BF16, acc = beta != 0.f;
+  const void* fn = bf ? (acc ? gemm_fn<true, true>() : gemm_fn<true, false>())
+                      : (acc ? gemm_fn<false, true>() : gemm_fn<false, false>());
+  int rc = set_max_dynamic_lds(fn, GM_LDS);
+  if (rc) return rc;
+  const dim3 grid((unsigned)(per_xcd_wg * GM_XCDS)), block(GM_NW * 64);
+  hipStream_t st = (hipStream_t)stream;
+  if (bf) {
+    if (acc) hipLaunchKernelGGL((gemm_bf16_kernel<true, true>), grid, block, GM_LDS, st, p);
+    else hipLaunchKernelGGL((gemm_bf16_kernel<true, false>), grid, block, GM_LDS, st, p);
+  } else {
+    if (acc) hipLaunchKernelGGL((gemm_bf16_kernel<false, true>), grid, block, GM_LDS, st, p);
+    else hipLaunchKernelGGL((gemm_bf16_kernel<false, false>), grid, block, GM_LDS, st, p);
+  }
+  INL_HIP_TRY(hipGetLastError());
+  return INL_OK;
+}

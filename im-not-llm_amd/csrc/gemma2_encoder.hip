@@ -11,7 +11,8 @@
 //           embedding and Wple_i this layer's rows of the per-layer-input
 //           projection (:625-628, one layer's slice at a time)
 //     x   = rms_norm(h) * input_norm
-//     qkv = x . [Wq; Wk; Wv]^T                   (inl_linear_fwd)
+//     qkv = x . [Wq; Wk; Wv]^T                   (inl_gemm_bf16_fwd in bf16,
+//                                                 inl_linear_fwd in f32)
 //     q, k = rope(rms_norm(q|k) * q|k_norm); v = rms_norm(v)   (:389-408,
 //                                                 inl_norm_rope_fwd)
 //     a   = attention, scale 1, bidirectional; sliding layers windowed
@@ -161,6 +162,28 @@ __global__ __launch_bounds__(256) void cast_kernel(int64_t n, const float* x, ch
 
 int grid_for(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256, 8192); }
 
+// Row counts above which a forward is refused when any of its GEMMs would go
+// to hipBLASLt (f32 runners, or bf16 shapes outside the hand-written GEMM's
+// limits): hipBLASLt's own initialisation failed ("Could not initialize
+// Tensile host") in the one configuration-3 run that reached it with
+// 139,124 rows, and the process then crashed inside the library; the
+// largest row count it has passed tests with here is 1,408.
+constexpr int64_t kLibGemmMaxRows = 16384;
+
+bool own_gemm_ok(int64_t n, int64_t k, int64_t xs, int64_t ws, int64_t ys) {
+  return k % 32 == 0 && n % 8 == 0 && xs % 8 == 0 && ws % 8 == 0 && ys % 8 == 0;
+}
+
+// The runner's GEMMs: bf16 ones on the hand-written kernel when the shape is
+// within its limits (every shape of the real EmbeddingGemma 2 text tower is),
+// f32 ones and any other shape on hipBLASLt (inl_linear_fwd).
+int gemm(int32_t dt, int64_t m, int64_t n, int64_t k, const void* x, int64_t xs, const void* w, int64_t ws,
+         int32_t out_dt, void* y, int64_t ys, float alpha, void* gws, size_t gws_bytes, void* stream) {
+  if (dt == INL_BF16 && own_gemm_ok(n, k, xs, ws, ys))
+    return inl_gemm_bf16_fwd(m, n, k, x, xs, w, ws, out_dt, y, ys, alpha, 0.f, stream);
+  return inl_linear_fwd(m, n, k, dt, x, xs, w, ws, out_dt, y, ys, alpha, 0.f, gws, gws_bytes, stream);
+}
+
 int launch_post_add(int dt, int64_t rows, int32_t dim, float* h, const float* t, const void* w1, const void* scalar,
                     float eps, const void* w2, void* x, hipStream_t st) {
   if (rows == 0) return INL_OK;
@@ -281,6 +304,22 @@ int layout(const inl_gemma2* e, int32_t n_texts, const int32_t* cu, Layout* L) {
   return INL_OK;
 }
 
+// Whether every GEMM of an encode goes to the hand-written bf16 kernel.
+bool all_own_gemms(const inl_gemma2* e, const Layout& L) {
+  const inl_gemma2_config& c = e->cfg;
+  if (c.dtype != INL_BF16) return false;
+  const int64_t H = c.hidden, I = c.intermediate, E = c.ple_dim;
+  bool ok = own_gemm_ok(E, H, H, H, E) && own_gemm_ok(2 * I, H, H, H, L.a_w) && own_gemm_ok(H, I, L.b_w, I, H) &&
+            own_gemm_ok(E, H, H, H, L.a_w) && own_gemm_ok(H, E, L.b_w, E, H) &&
+            own_gemm_ok(c.embedding_dim, H, H, H, c.embedding_dim);
+  for (int i = 0; i < c.layers && ok; ++i) {
+    const LayerShape s = shape_of(e, i);
+    const int64_t qd = (int64_t)c.heads * s.hd, kvd = (int64_t)s.kvh * s.hd;
+    ok = own_gemm_ok(qd + 2 * kvd, H, H, H, L.a_w) && own_gemm_ok(H, qd, L.b_w, qd, H);
+  }
+  return ok;
+}
+
 int check_config(const inl_gemma2_config* c) {
   if (!c) return fail(INL_E_INVALID, "gemma2: config is NULL");
   if (c->vocab <= 0 || c->hidden <= 0 || c->intermediate <= 0 || c->layers <= 0 || c->heads <= 0 ||
@@ -296,10 +335,11 @@ int check_config(const inl_gemma2_config* c) {
 }
 
 int check_shape(const inl_gemma2_config* c, int i, int hd, int kvh) {
-  const bool pow2 = hd >= 8 && hd <= 512 && hd % 8 == 0 && ((hd / 8) & (hd / 8 - 1)) == 0;
+  // the attention kernels take head_dim up to 256 (inl_attn_* refuses more)
+  const bool pow2 = hd >= 8 && hd <= 256 && hd % 8 == 0 && ((hd / 8) & (hd / 8 - 1)) == 0;
   if (!pow2 || kvh <= 0 || c->heads % kvh)
     return fail(INL_E_UNSUPPORTED, "gemma2: layer " + std::to_string(i) + ": head_dim must be 8 x a power of two "
-                                   "up to 512 and the KV heads must divide the heads");
+                                   "up to 256 and the KV heads must divide the heads");
   return INL_OK;
 }
 
@@ -418,6 +458,11 @@ extern "C" int inl_gemma2_encode(inl_gemma2* e, int32_t n_texts, const int32_t* 
   if (!workspace || workspace_bytes < L.total || ((uintptr_t)workspace & 255))
     return fail(INL_E_INVALID,
                 "gemma2: workspace is NULL, unaligned (256 B) or smaller than inl_gemma2_workspace_size()");
+  if (n > kLibGemmMaxRows && !all_own_gemms(e, L))
+    return fail(INL_E_UNSUPPORTED, "gemma2: " + std::to_string(n) + " tokens: batches above " +
+                                       std::to_string(kLibGemmMaxRows) +
+                                       " tokens run only when every GEMM is on the library's own bf16 kernel "
+                                       "(bf16 weights, widths and strides multiples of 8, inner sizes of 32)");
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   int32_t* d_ids = (int32_t*)(ws + L.ids);
@@ -484,11 +529,11 @@ extern "C" int inl_gemma2_encode(inl_gemma2* e, int32_t n_texts, const int32_t* 
     const size_t pk = std::find(L.keys.begin(), L.keys.end(), AttnKey{s.full ? -1 : c.sliding_window, s.hd, s.kvh}) -
                       L.keys.begin();
     // this layer's per-layer input
-    if (!rc) rc = inl_linear_fwd(n, E, H, dt, x0, H, (const char*)e->ple_proj + (int64_t)i * E * H * es, H, INL_F32,
-                                 T, E, 1.0f / std::sqrt((float)c.hidden), 0.f, gws, gws_bytes, stream);
+    if (!rc) rc = gemm(dt, n, E, H, x0, H, (const char*)e->ple_proj + (int64_t)i * E * H * es, H, INL_F32, T, E,
+                       1.0f / std::sqrt((float)c.hidden), gws, gws_bytes, stream);
     if (!rc) rc = inl_rms_norm_rows_fwd(n, c.ple_dim, T, E, e->ple_norm, dt, c.eps, dt, P, E, stream);
     if (i == 0 && !rc) rc = inl_rms_norm_rows_fwd(n, c.hidden, h, H, w.input_norm, dt, c.eps, dt, x, H, stream);
-    if (!rc) rc = inl_linear_fwd(n, qkv_w, H, dt, x, H, w.qkv_proj, H, dt, A, L.a_w, 1.f, 0.f, gws, gws_bytes, stream);
+    if (!rc) rc = gemm(dt, n, qkv_w, H, x, H, w.qkv_proj, H, dt, A, L.a_w, 1.f, gws, gws_bytes, stream);
     nr.head_dim = s.hd;
     nr.rotary_dim = s.hd;
     nr.heads = c.heads;
@@ -501,19 +546,16 @@ extern "C" int inl_gemma2_encode(inl_gemma2* e, int32_t n_texts, const int32_t* 
     if (!rc) rc = inl_norm_rope_fwd(&nr, A + (qd + kvd) * es, A + (qd + kvd) * es, nullptr, d_pos, nullptr, nullptr,
                                     nullptr, nullptr, stream);
     if (!rc) rc = inl_attn_fwd(plans[pk], A, A + qd * es, A + (qd + kvd) * es, B, stream);
-    if (!rc) rc = inl_linear_fwd(n, H, qd, dt, B, L.b_w, w.o_proj, qd, INL_F32, T, H, 1.f, 0.f, gws, gws_bytes, stream);
+    if (!rc) rc = gemm(dt, n, H, qd, B, L.b_w, w.o_proj, qd, INL_F32, T, H, 1.f, gws, gws_bytes, stream);
     if (!rc) rc = launch_post_add(dt, n, c.hidden, h, T, w.post_attention_norm, nullptr, c.eps, w.pre_feedforward_norm,
                                   x, st);
-    if (!rc) rc = inl_linear_fwd(n, 2 * I, H, dt, x, H, w.gate_up_proj, H, dt, A, L.a_w, 1.f, 0.f, gws, gws_bytes,
-                                 stream);
+    if (!rc) rc = gemm(dt, n, 2 * I, H, x, H, w.gate_up_proj, H, dt, A, L.a_w, 1.f, gws, gws_bytes, stream);
     if (!rc) rc = launch_gelu_gate(dt, n, c.intermediate, A, L.a_w, A + I * es, L.a_w, B, L.b_w, st);
-    if (!rc) rc = inl_linear_fwd(n, H, I, dt, B, L.b_w, w.down_proj, I, INL_F32, T, H, 1.f, 0.f, gws, gws_bytes, stream);
+    if (!rc) rc = gemm(dt, n, H, I, B, L.b_w, w.down_proj, I, INL_F32, T, H, 1.f, gws, gws_bytes, stream);
     if (!rc) rc = launch_post_add(dt, n, c.hidden, h, T, w.post_feedforward_norm, nullptr, c.eps, nullptr, x, st);
-    if (!rc) rc = inl_linear_fwd(n, E, H, dt, x, H, w.ple_input_gate, H, dt, A, L.a_w, 1.f, 0.f, gws, gws_bytes,
-                                 stream);
+    if (!rc) rc = gemm(dt, n, E, H, x, H, w.ple_input_gate, H, dt, A, L.a_w, 1.f, gws, gws_bytes, stream);
     if (!rc) rc = launch_gelu_gate(dt, n, c.ple_dim, A, L.a_w, P, E, B, L.b_w, st);
-    if (!rc) rc = inl_linear_fwd(n, H, E, dt, B, L.b_w, w.ple_projection, E, INL_F32, T, H, 1.f, 0.f, gws, gws_bytes,
-                                 stream);
+    if (!rc) rc = gemm(dt, n, H, E, B, L.b_w, w.ple_projection, E, INL_F32, T, H, 1.f, gws, gws_bytes, stream);
     const void* next_norm = i + 1 < c.layers ? e->layers[i + 1].input_norm : e->final_norm;
     if (!rc) rc = launch_post_add(dt, n, c.hidden, h, T, w.ple_post_norm, w.layer_scalar, c.eps, next_norm, x, st);
   }
@@ -528,8 +570,8 @@ extern "C" int inl_gemma2_encode(inl_gemma2* e, int32_t n_texts, const int32_t* 
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) rc = hip_fail(err, "gemma2: pooled cast");
   }
-  if (!rc) rc = inl_linear_fwd(n_texts, c.embedding_dim, H, dt, pooled_dt, H, e->emb_proj, H, INL_F32, proj,
-                               c.embedding_dim, 1.f, 0.f, gws, gws_bytes, stream);
+  if (!rc) rc = gemm(dt, n_texts, c.embedding_dim, H, pooled_dt, H, e->emb_proj, H, INL_F32, proj, c.embedding_dim, 1.f, gws,
+                     gws_bytes, stream);
   if (!rc) {
     if (out_dim == c.embedding_dim) {
       rc = inl_l2_normalize_fwd(n_texts, c.embedding_dim, c.embedding_dim, proj, out_dim, out, 1e-12f, 0, stream);

@@ -511,8 +511,12 @@ def pool_splade(logits, offs, *, bias=None, shift=0.0, masked_ids=(), canonical=
 # ---------------------------------------------------------------------------
 
 _linear_ws = _sig("inl_linear_workspace_size", ctypes.c_int, ctypes.POINTER(ctypes.c_size_t))
+_linear_stats = _sig("inl_linear_stats", ctypes.c_int, ctypes.POINTER(c_i64), ctypes.POINTER(c_i64),
+                     ctypes.POINTER(c_i64))
 _linear = _sig("inl_linear_fwd", ctypes.c_int, c_i64, c_i64, c_i64, c_i32, c_void_p, c_i64, c_void_p, c_i64,
                c_i32, c_void_p, c_i64, ctypes.c_float, ctypes.c_float, c_void_p, ctypes.c_size_t, c_void_p)
+_gemm = _sig("inl_gemm_bf16_fwd", ctypes.c_int, c_i64, c_i64, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i32,
+             c_void_p, c_i64, ctypes.c_float, ctypes.c_float, c_void_p)
 _embed = _sig("inl_embed_fwd", ctypes.c_int, c_i64, c_void_p, c_void_p, c_i64, c_i32, c_i32, c_void_p, c_i64,
               c_void_p)
 _rms_rows = _sig("inl_rms_norm_rows_fwd", ctypes.c_int, c_i64, c_i32, c_void_p, c_i64, c_void_p, c_i32,
@@ -574,6 +578,35 @@ def linear(x, w, *, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=None):
                    _dtype_code(out.dtype), out.data_ptr(), out.stride(0), float(alpha), float(beta),
                    ws.data_ptr(), ws.numel(), _stream_ptr(stream)))
     return out
+
+
+def gemm_bf16(x, w, *, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=None):
+    """``out = alpha * x @ w.T + beta * out`` on the library's own bf16 MFMA
+    kernel (``inl_gemm_bf16_fwd``): bf16 ``x [m, k]`` and ``w [n, k]``, rows
+    may be strided; ``out`` f32 or bf16."""
+    import torch
+    m, k = x.shape
+    n = w.shape[0]
+    if w.shape[1] != k or x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise InlError(-1, "gemm_bf16: x [m, k] and w [n, k] must be bf16 and agree in k")
+    if x.stride(1) != 1 or w.stride(1) != 1:
+        raise InlError(-1, "gemm_bf16: rows must be contiguous")
+    od = out_dtype if out_dtype is not None else (out.dtype if out is not None else torch.bfloat16)
+    if out is None:
+        out = torch.empty((m, n), dtype=od, device=x.device)
+    if out.shape != (m, n) or out.stride(1) != 1:
+        raise InlError(-1, f"gemm_bf16: out must be [{m}, {n}] with contiguous rows")
+    _check(_gemm(m, n, k, x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), _dtype_code(out.dtype),
+                 out.data_ptr(), out.stride(0), float(alpha), float(beta), _stream_ptr(stream)))
+    return out
+
+
+def linear_stats():
+    """``inl_linear_stats``: dict of hipBLASLt timing passes run so far, (shape,
+    row-count bucket) choices held and exact-row-count entries cached."""
+    t, b, c = c_i64(), c_i64(), c_i64()
+    _check(_linear_stats(ctypes.byref(t), ctypes.byref(b), ctypes.byref(c)))
+    return {"tunings": t.value, "buckets": b.value, "cached_shapes": c.value}
 
 
 def embed(ids, table, *, stream=None):

@@ -33,18 +33,39 @@ extern "C" {
  * o_proj and down_proj GEMMs. dtypes: f32 -> f32, bf16 -> bf16, bf16 -> f32.
  * Strides are elements between rows (0 = packed). `workspace` (device, may be
  * NULL with 0 bytes) lets hipBLASLt pick kernels that need scratch; size it
- * with inl_linear_workspace_size. Runs hipBLASLt; per device and shape the
- * first call queries its heuristic and, unless `stream` is capturing a
- * graph, times up to 16 of its candidates on the call's operands (into a
- * scratch output it allocates and frees; y is not touched) and keeps the
- * fastest. That first call synchronises the stream; later calls reuse the
- * choice and allocate nothing. */
+ * with inl_linear_workspace_size. Runs hipBLASLt. Row counts m fall in
+ * power-of-two buckets ((2^(b-1), 2^b], m <= 64 in one): per device, shape
+ * (n, k, strides, dtypes, beta != 0, workspace) and bucket, the first call
+ * queries the heuristic and, unless `stream` is capturing a graph, times up
+ * to 16 of its candidates on the call's operands (into a scratch output it
+ * allocates and frees; y is not touched) and keeps the fastest. That call
+ * synchronises the stream. Any other m of the bucket reuses the choice once
+ * hipBLASLt confirms it supports that m (host-side only: no allocation, no
+ * synchronisation, no device work besides the GEMM); the per-m layouts are
+ * cached, the oldest of 512 evicted first. */
 int inl_linear_workspace_size(size_t* bytes);
+/* Diagnostics of inl_linear_fwd's cache (process-wide, all devices): timing
+ * passes run so far, (shape, bucket) choices held, exact-m entries held. Any
+ * out-pointer may be NULL. No reference counterpart. */
+int inl_linear_stats(int64_t* tunings, int64_t* buckets, int64_t* cached_shapes);
 int inl_linear_fwd(int64_t m, int64_t n, int64_t k, int32_t in_dtype,
                    const void* x, int64_t x_stride, const void* w,
                    int64_t w_stride, int32_t out_dtype, void* y,
                    int64_t y_stride, float alpha, float beta, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/* y = alpha * x . w^T + beta * y on the matrix cores, bf16 x [m, k] and
+ * w [n, k] rows (row strides in elements, 0 = packed), f32 accumulation,
+ * y [m, n] rows in out_dtype (f32 or bf16). The same bias-free Linear as
+ * inl_linear_fwd (candle_nn::Linear through linear_no_bias,
+ * crates/inl-text/src/qwen3/mod.rs:99-104, crates/inl-text/src/gemma2.rs:
+ * 233-283), as one hand-written kernel: no workspace, no allocation, no
+ * tuning, no synchronisation, for every m (graph-capturable). k a multiple
+ * of 32, n and the strides multiples of 8, pointers 16-byte aligned. */
+int inl_gemm_bf16_fwd(int64_t m, int64_t n, int64_t k, const void* x,
+                      int64_t x_stride, const void* w, int64_t w_stride,
+                      int32_t out_dtype, void* y, int64_t y_stride,
+                      float alpha, float beta, void* stream);
 
 /* out[t, :] = f32(table[ids[t], :]): the token embedding (candle Embedding,
  * qwen3/mod.rs:322-323,350) into an f32 residual stream. ids are device

@@ -192,6 +192,9 @@ void sizers_and_refusals() {
   lw[1].head_dim = 24;
   expect(inl_gemma2_create(&gc, dummy, lw.data(), dummy, dummy, dummy, dummy, &g) < 0 && !g,
          "gemma2 refuses a head_dim override that is not 8 x a power of two");
+  lw[1].head_dim = 512;  // 8 x a power of two, but beyond the attention kernels' 256
+  expect(inl_gemma2_create(&gc, dummy, lw.data(), dummy, dummy, dummy, dummy, &g) < 0 && !g,
+         "gemma2 refuses a head_dim above 256");
   lw[1].head_dim = 32;   // both layers sliding: 16 and 32 cannot share the kind's one RoPE table
   expect(inl_gemma2_create(&gc, dummy, lw.data(), dummy, dummy, dummy, dummy, &g) < 0 && !g,
          "gemma2 refuses two head dims within one layer kind");

@@ -211,10 +211,39 @@ def test_asm_load_kernels_use_no_scratch():
             "x.hip:90:1: remark: Function Name: _Z1jv [-Rpass-analysis=kernel-resource-usage]\n"
             "x.hip:90:1: remark:     ScratchSize [bytes/lane]: 284 [-Rpass-analysis=kernel-resource-usage]\n")
     assert b.scratch_users(text) == ["_Z1jv (284 B/lane)"]
+    with pytest.raises(RuntimeError, match="use scratch"):
+        b.check_no_scratch("x.hip", text)
+    # no remarks at all (flag ignored, remarks elsewhere) and a block with no
+    # ScratchSize line both fail the check instead of passing it
+    with pytest.raises(RuntimeError, match="no kernel-resource-usage remarks"):
+        b.check_no_scratch("x.hip", "")
+    with pytest.raises(RuntimeError, match="without a ScratchSize"):
+        b.check_no_scratch("x.hip", text.splitlines()[0] + "\n")
+    b.check_no_scratch("x.hip", "\n".join(text.splitlines()[:3]))
     asm_loads = {p.name for p in (ROOT / "im-not-llm_amd" / "csrc").glob("*.hip")
                  if re.search(r'asm volatile\("buffer_load', p.read_text())
                  or re.search(r'vmcnt\(%', p.read_text()) or '"attn_stream.hpp"' in p.read_text()}
     assert asm_loads <= b.NO_SCRATCH, asm_loads - b.NO_SCRATCH
+
+
+def test_no_scratch_remarks_are_parsed_from_a_real_compile(tmp_path):
+    """Compile the smallest no-scratch source with the build's own flags and
+    remark options: the compiler's remarks must describe its kernels, so the
+    build's check sees real input, not an empty string."""
+    import importlib.util
+    import subprocess
+    spec = importlib.util.spec_from_file_location("inl_build", ROOT / "im-not-llm_amd" / "build.py")
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    src = ROOT / "im-not-llm_amd" / "csrc" / "splade_decoder.hip"
+    assert src.name in b.NO_SCRATCH
+    r = subprocess.run([b.HIPCC, *b.FLAGS, "-c", *b.RESOURCE_REMARKS, str(src), "-o", str(tmp_path / "s.o")],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    parsed = b.parse_scratch(r.stderr)
+    kernels = [n for n, _ in parsed if "splade_decoder_max_kernel" in n]
+    assert kernels and all(s == 0 for _, s in parsed), parsed
+    b.check_no_scratch(src.name, r.stderr)
 
 
 def test_small_f32_batches_split_their_key_ranges():

@@ -62,6 +62,37 @@ def test_linear_bf16(out, cuda, inl):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_linear_one_tuning_per_row_bucket(dtype, cuda, inl):
+    """50 distinct row counts of one shape, all in the bucket (256, 512]: at
+    most one timing pass for the shape, every product still exact to the
+    same bound as the single-shape tests. A row count of another bucket adds
+    at most one more pass; a repeated row count adds none."""
+    import torch
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    n, k = 640, 384   # a shape no other test uses, so its bucket starts untimed
+    w = _rand(torch, cuda, (n, k), 11, k ** -0.5).to(td)
+    xall = _rand(torch, cuda, (600, k), 12).to(td)
+    before = inl.linear_stats()
+    print(f"case=linear_buckets {dtype} stats before {before}", flush=True)
+    worst = 0.0
+    for m in range(300, 350):
+        x = xall[:m]
+        y = inl.linear(x, w, out_dtype=torch.float32)
+        ref = x.double() @ w.double().T
+        torch.cuda.synchronize()
+        worst = max(worst, (y.double() - ref).abs().max().item() / ref.abs().max().item())
+    mid = inl.linear_stats()
+    assert mid["tunings"] - before["tunings"] <= 1, (before, mid)
+    assert worst <= (1e-5 if dtype == "f32" else 1e-4), worst
+    for m in (349, 520, 349):   # repeated: cached; 520: bucket (512, 1024]
+        inl.linear(xall[:m], w, out_dtype=torch.float32)
+    after = inl.linear_stats()
+    print(f"case=linear_buckets {dtype} stats after {after}", flush=True)
+    assert after["tunings"] - mid["tunings"] <= 1, (mid, after)
+    assert after["cached_shapes"] <= 512
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_embed_rms_swiglu(dtype, cuda, inl):
     import torch
     td = torch.float32 if dtype == "f32" else torch.bfloat16
