@@ -37,9 +37,10 @@ fp32 vector peak. The
 end-to-end workloads (--workload qwen3_e2e, f32 as configuration 1, and
 qwen3_e2e_bf16) time a whole Qwen3-0.6B encode of 8 texts (778 tokens) and
 report encoded tokens/s, with the numpy f32 forward as the CPU baseline;
---workload gemma_e2e would do the same for configuration 3 (the
-EmbeddingGemma-2 text tower, bf16, 32 texts of U[64,8192] tokens); it is
-switched off for now (see gemma_e2e_main).
+--workload gemma_e2e does the same for configuration 3 (the
+EmbeddingGemma-2 text tower, bf16, 32 texts of U[64,8192] tokens, every GEMM
+on the library's own bf16 kernel), with three of its texts checked against
+the oracle.
 """
 from __future__ import annotations
 
@@ -336,13 +337,9 @@ def gemma_e2e_main(args):
     heads x 256, sliding radius 512 with every sixth layer full) on 32 texts
     of U[64, 8192] tokens, bf16; embed -> per-layer inputs -> 24 layers ->
     mean pool -> projection -> L2; one step = one encode."""
-    # Switched off: the one full-size run (139,124 tokens) ended in a GPU memory
-    # fault, after hipBLASLt printed "Could not initialize Tensile host:
-    # unordered_map::at" and before any step completed. The runner's tests at
-    # smaller sizes pass; no cause in this library's code has been found yet,
-    # so the full-size encode stays off the GPU until one is.
-    raise SystemExit("bench.py: --workload gemma_e2e is switched off: its full-size encode faulted the GPU "
-                     "once and the cause is not found yet")
+    # Every GEMM of this workload runs on the library's own bf16 kernel
+    # (inl_gemm_bf16_fwd); the runner refuses batches this large whenever
+    # one would go to hipBLASLt.
     import numpy as np
     import torch
     import inl_hip
@@ -399,13 +396,37 @@ def gemma_e2e_main(args):
                    "value_is": "end-to-end encoded tokens/s (embed, 24 layers, pooling, projection, L2 per step)"},
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "whole encode (hipBLASLt GEMMs, attention, prologue, norms, GEGLU, pooling)",
+                     "kernel": "whole encode (own bf16 MFMA GEMMs, attention, prologue, norms, GEGLU, pooling)",
                      "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"flop": flops}},
     }
+    result["parity"] = gemma_e2e_parity(host_w, tc, ids, cu, out, weights)
     if not args.no_cpu:
         result["cpu_baseline"] = gemma_e2e_cpu_baseline(host_w, tc, args.cpu_seconds)
     enc.close()
     print(json.dumps(result), flush=True)
+
+
+def gemma_e2e_parity(host_w, tc, ids, cu, out, weights):
+    """Cosines of three texts of the timed batch (the shortest and the two
+    nearest 1,000 tokens) against oracle/gemma2.py in f32 on the bf16-rounded
+    weights: texts are independent in a packed batch, so the oracle encodes
+    just those texts. The reference's bf16 floor is cosine >= 0.999."""
+    import numpy as np
+    from oracle import gemma2 as og
+    lens = np.diff(np.asarray(cu))
+    order = [int(np.argmin(lens))] + [int(i) for i in np.argsort(np.abs(lens - 1000))[:3]]
+    picks = list(dict.fromkeys(order))[:3]
+    wb = {k: v.float().cpu().numpy() for k, v in weights.items()}
+    sub_ids = np.concatenate([ids[cu[b]:cu[b + 1]] for b in picks])
+    sub_cu = np.concatenate([[0], np.cumsum([lens[b] for b in picks])])
+    t0 = time.perf_counter()
+    ref = og.encode(wb, tc, sub_ids, sub_cu, dtype=np.float32).astype(np.float64)
+    got = out[picks].double().cpu().numpy()
+    cos = (got * ref).sum(1) / np.linalg.norm(got, axis=1) / np.linalg.norm(ref, axis=1)
+    log(f"gemma_e2e parity: texts {picks} ({[int(lens[b]) for b in picks]} tokens): cosines "
+        f"{[round(float(c), 6) for c in cos]} ({time.perf_counter() - t0:.1f} s)")
+    return {"texts": picks, "tokens": [int(lens[b]) for b in picks], "cosine": [round(float(c), 6) for c in cos],
+            "against": "oracle/gemma2.py f32 on the bf16-rounded weights", "min_cosine": round(float(cos.min()), 6)}
 
 
 def op_workload(name, torch, inl_hip, dev):

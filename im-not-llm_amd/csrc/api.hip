@@ -1,4 +1,5 @@
 // Error reporting and argument checks shared by the library's entry points.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -34,6 +35,38 @@ int check_cu(int32_t n, const int32_t* cu, int64_t* total) {
   for (int32_t b = 0; b < n; ++b)
     if (cu[b + 1] < cu[b]) return fail(INL_E_INVALID, "cu_seqlens must be nondecreasing");
   *total = cu[n];
+  return INL_OK;
+}
+
+HostStage::~HostStage() {
+  if (done) {
+    if (pending) (void)hipEventSynchronize(done);
+    (void)hipEventDestroy(done);
+  }
+  if (buf) (void)hipHostFree(buf);
+}
+
+int HostStage::reserve(size_t bytes) {
+  if (pending) {
+    INL_HIP_TRY(hipEventSynchronize(done));
+    pending = false;
+  }
+  if (!done) INL_HIP_TRY(hipEventCreateWithFlags(&done, hipEventDisableTiming));
+  if (bytes <= cap) return INL_OK;
+  if (buf) {
+    INL_HIP_TRY(hipHostFree(buf));
+    buf = nullptr;
+    cap = 0;
+  }
+  const size_t want = std::max<size_t>(bytes + bytes / 4, (size_t)1 << 16);
+  INL_HIP_TRY(hipHostMalloc((void**)&buf, want, hipHostMallocDefault));
+  cap = want;
+  return INL_OK;
+}
+
+int HostStage::record(hipStream_t st) {
+  INL_HIP_TRY(hipEventRecord(done, st));
+  pending = true;
   return INL_OK;
 }
 

@@ -1206,6 +1206,7 @@ int launch_one_shot(const inl_attn_desc* desc, const Schedule& s, void* buf, con
 struct inl_attn_plan {
   inl_attn_desc desc;     // cu_seqlens_host and seq_starts_host are not kept
   inl::Schedule sched;    // also kept on the host for inspection
+  std::vector<char> host_blob;   // the uploaded schedule bytes (inl_attn_plan_create_in), kept with the plan
   void* d_sched = nullptr;
   bool owns_sched = true; // false: d_sched is the caller's workspace
   int64_t total_tokens = 0;
@@ -1239,11 +1240,13 @@ extern "C" int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** p
   return INL_OK;
 }
 
-extern "C" int inl_attn_plan_create_in(const inl_attn_desc* desc, void* workspace, size_t workspace_bytes,
-                                       void* stream, inl_attn_plan** plan) {
-  using namespace inl;
-  if (!plan) return fail(INL_E_INVALID, "attention: plan out-pointer is NULL");
+namespace inl {
+
+int attn_plan_prepare(const inl_attn_desc* desc, void* dev_sched, size_t workspace_bytes, std::vector<char>* blob,
+                      inl_attn_plan** plan) {
+  if (!plan || !blob) return fail(INL_E_INVALID, "attention: plan out-pointer is NULL");
   *plan = nullptr;
+  blob->clear();
   int64_t total = 0;
   int rc = validate_desc(desc, &total);
   if (rc) return rc;
@@ -1256,20 +1259,41 @@ extern "C" int inl_attn_plan_create_in(const inl_attn_desc* desc, void* workspac
   pl->owns_sched = false;
   rc = build_schedule(desc, &pl->sched);
   if (!rc) rc = ensure_lds_attr(pl->sched.cfg);
-  const std::vector<char> blob = rc ? std::vector<char>() : pl->sched.pack();
-  if (!rc && !blob.empty()) {
-    if (!workspace || workspace_bytes < pl->sched.bytes())
+  if (!rc) *blob = pl->sched.pack();
+  if (!rc && !blob->empty()) {
+    if (!dev_sched || workspace_bytes < pl->sched.bytes())
       rc = fail(INL_E_INVALID, "attention: workspace is NULL or smaller than inl_attn_workspace_size()");
-    else if (!aligned16(workspace))
+    else if (!aligned16(dev_sched))
       rc = fail(INL_E_INVALID, "attention: workspace must be 16-byte aligned");
-    else {
-      hipError_t e = hipMemcpyAsync(workspace, blob.data(), blob.size(), hipMemcpyHostToDevice, (hipStream_t)stream);
-      if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(plan)");
-      pl->d_sched = workspace;
-    }
+    else
+      pl->d_sched = dev_sched;
   }
-  if (rc) { delete pl; return rc; }
+  if (rc) {
+    delete pl;
+    blob->clear();
+    return rc;
+  }
   *plan = pl;
+  return INL_OK;
+}
+
+}  // namespace inl
+
+extern "C" int inl_attn_plan_create_in(const inl_attn_desc* desc, void* workspace, size_t workspace_bytes,
+                                       void* stream, inl_attn_plan** plan) {
+  using namespace inl;
+  std::vector<char> blob;
+  int rc = attn_plan_prepare(desc, workspace, workspace_bytes, &blob, plan);
+  if (rc || blob.empty()) return rc;
+  // the plan keeps the host copy of its schedule until it is destroyed
+  (*plan)->host_blob = std::move(blob);
+  const hipError_t e = hipMemcpyAsync(workspace, (*plan)->host_blob.data(), (*plan)->host_blob.size(),
+                                      hipMemcpyHostToDevice, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    delete *plan;
+    *plan = nullptr;
+    return hip_fail(e, "hipMemcpyAsync(plan)");
+  }
   return INL_OK;
 }
 

@@ -33,6 +33,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <tuple>
@@ -53,6 +54,8 @@ struct inl_gemma2 {
   int hd_kind[2] = {0, 0};            // head_dim of the RoPE table of sliding (0) and full (1) layers
   float* cos[2] = {nullptr, nullptr};  // device, owned: [max_positions, hd_kind / 2]
   float* sin[2] = {nullptr, nullptr};
+  std::mutex mu;                       // one encode at a time (the staging buffer is shared)
+  inl::HostStage stage;                // pinned source of the per-call uploads
 };
 
 namespace inl {
@@ -483,17 +486,49 @@ extern "C" int inl_gemma2_encode(inl_gemma2* e, int32_t n_texts, const int32_t* 
   rc = inl_linear_workspace_size(&gws_bytes);
   if (rc) return rc;
 
-  std::vector<int32_t> pos(n);
-  rc = inl_positions_host(n_texts, cu, pos.data());
-  if (rc) return rc;
-  INL_HIP_TRY(hipMemcpyAsync(d_ids, ids_host, n * 4, hipMemcpyHostToDevice, st));
-  INL_HIP_TRY(hipMemcpyAsync(d_pos, pos.data(), n * 4, hipMemcpyHostToDevice, st));
-  INL_HIP_TRY(hipMemcpyAsync(d_cu, cu, (size_t)(n_texts + 1) * 4, hipMemcpyHostToDevice, st));
-
+  // Uploads, all from the runner's pinned staging buffer: token ids,
+  // text-local positions and offsets (the workspace's first three regions,
+  // mirrored byte for byte in the buffer), then each attention plan's
+  // schedule (one plan per distinct layer shape, used by every layer of it).
+  std::lock_guard<std::mutex> lock(e->mu);
+  std::vector<std::vector<char>> blobs(L.keys.size());
   std::vector<inl_attn_plan*> plans(L.keys.size(), nullptr);
+  auto destroy_plans = [&]() {
+    int r = INL_OK;
+    for (inl_attn_plan* p : plans)
+      if (p) {
+        const int r2 = inl_attn_plan_destroy(p);
+        if (!r) r = r2;
+      }
+    return r;
+  };
   for (size_t k = 0; k < L.keys.size() && !rc; ++k) {
     const inl_attn_desc d = attn_desc(e, n_texts, cu, L.keys[k], L);
-    rc = inl_attn_plan_create_in(&d, ws + L.sched[k], L.sched_bytes[k], stream, &plans[k]);
+    rc = attn_plan_prepare(&d, ws + L.sched[k], L.sched_bytes[k], &blobs[k], &plans[k]);
+  }
+  const size_t head = L.cu + (size_t)(n_texts + 1) * 4;   // L.ids == 0
+  size_t need = up256(head);
+  for (const std::vector<char>& b : blobs) need += up256(b.size());
+  if (!rc) rc = e->stage.reserve(need);
+  if (!rc) {
+    char* hb = e->stage.buf;
+    std::memcpy(hb + L.ids, ids_host, (size_t)n * 4);
+    rc = inl_positions_host(n_texts, cu, (int32_t*)(hb + L.pos));
+    std::memcpy(hb + L.cu, cu, (size_t)(n_texts + 1) * 4);
+    hipError_t err = rc ? hipSuccess : hipMemcpyAsync(ws, hb, head, hipMemcpyHostToDevice, st);
+    size_t off = up256(head);
+    for (size_t k = 0; k < blobs.size() && !rc && err == hipSuccess; ++k) {
+      if (blobs[k].empty()) continue;
+      std::memcpy(hb + off, blobs[k].data(), blobs[k].size());
+      err = hipMemcpyAsync(ws + L.sched[k], hb + off, blobs[k].size(), hipMemcpyHostToDevice, st);
+      off += up256(blobs[k].size());
+    }
+    if (err != hipSuccess) rc = hip_fail(err, "gemma2: uploads");
+    if (!rc) rc = e->stage.record(st);
+  }
+  if (rc) {
+    (void)destroy_plans();
+    return rc;
   }
 
   const int dt = c.dtype, es = dtype_size(dt);
@@ -581,10 +616,6 @@ extern "C" int inl_gemma2_encode(inl_gemma2* e, int32_t n_texts, const int32_t* 
       if (!rc) rc = inl_l2_normalize_fwd(n_texts, out_dim, c.embedding_dim, proj, out_dim, out, 0.f, 1, stream);
     }
   }
-  for (inl_attn_plan* p : plans)
-    if (p) {
-      const int rc2 = inl_attn_plan_destroy(p);
-      if (!rc) rc = rc2;
-    }
-  return rc;
+  const int rc2 = destroy_plans();
+  return rc ? rc : rc2;
 }

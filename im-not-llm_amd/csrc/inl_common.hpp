@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/inl_hip.h"
 
@@ -49,5 +50,33 @@ int check_cu(int32_t n, const int32_t* cu, int64_t* total);
 int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const void* weight,
                      const void* weight2, int32_t w2_heads, const int32_t* rows, const float* cos,
                      const float* sin, const float* cos2, const float* sin2, void* stream);
+
+// Pinned host staging for a runner's per-call uploads (token ids, positions,
+// offsets, attention schedules). A call waits until the copies of the
+// previous call have consumed the buffer (one event), fills it, issues its
+// hipMemcpyAsync calls from it and records the event again: the source of
+// every copy outlives the copy, and the copies are truly asynchronous (no
+// pageable staging inside the runtime). The buffer grows on demand (pinned
+// allocations happen only then) and is freed with the runner.
+struct HostStage {
+  char* buf = nullptr;
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  bool pending = false;
+  HostStage() = default;
+  HostStage(const HostStage&) = delete;
+  HostStage& operator=(const HostStage&) = delete;
+  ~HostStage();
+  // wait for the previous call's copies, then hold at least `bytes`
+  int reserve(size_t bytes);
+  // after this call's copies were issued on `st`
+  int record(hipStream_t st);
+};
+
+// inl_attn_plan_create_in without the upload: the plan reads its schedule
+// from `dev_sched` (workspace_bytes long), and `blob` receives the bytes the
+// caller must copy there before the plan's first launch.
+int attn_plan_prepare(const inl_attn_desc* desc, void* dev_sched, size_t workspace_bytes, std::vector<char>* blob,
+                      inl_attn_plan** plan);
 
 }  // namespace inl

@@ -60,6 +60,8 @@ struct inl_qwen3 {
   int g_runs = 0;                    // calls with this key so far
   hipGraphExec_t g_exec = nullptr;
   hipStream_t cap = nullptr;         // private capture stream (default priority)
+  std::mutex stage_mu;               // one call at a time fills the staging buffer
+  inl::HostStage stage;              // pinned source of the per-call uploads
 };
 
 namespace inl {
@@ -329,15 +331,6 @@ extern "C" int inl_qwen3_encode(inl_qwen3* e, int32_t n_texts, const int32_t* cu
   rc = inl_linear_workspace_size(&gws_bytes);
   if (rc) return rc;
 
-  // ids, text-local positions and offsets to the device (pageable copies:
-  // the host buffers may go when the calls return)
-  std::vector<int32_t> pos(n);
-  rc = inl_positions_host(n_texts, cu, pos.data());
-  if (rc) return rc;
-  INL_HIP_TRY(hipMemcpyAsync(d_ids, ids_host, n * 4, hipMemcpyHostToDevice, st));
-  INL_HIP_TRY(hipMemcpyAsync(d_pos, pos.data(), n * 4, hipMemcpyHostToDevice, st));
-  INL_HIP_TRY(hipMemcpyAsync(d_cu, cu, (size_t)(n_texts + 1) * 4, hipMemcpyHostToDevice, st));
-
   // the attention plan of this batch, used by every layer
   const int dt = c.dtype, es = dtype_size(dt);
   const int64_t qd = (int64_t)c.heads * c.head_dim, kvd = (int64_t)c.kv_heads * c.head_dim;
@@ -357,8 +350,35 @@ extern "C" int inl_qwen3_encode(inl_qwen3* e, int32_t n_texts, const int32_t* cu
   ad.o_row_stride = L.b_w;
   ad.flags = c.attn_flags;
   inl_attn_plan* plan = nullptr;
-  rc = inl_attn_plan_create_in(&ad, ws + L.sched, L.gemm - L.sched, stream, &plan);
+  std::vector<char> blob;
+  rc = attn_plan_prepare(&ad, ws + L.sched, L.gemm - L.sched, &blob, &plan);
   if (rc) return rc;
+
+  // Uploads from the runner's pinned staging buffer: ids, text-local
+  // positions and offsets (the workspace's first three regions, mirrored byte
+  // for byte), then the plan's schedule.
+  {
+    std::lock_guard<std::mutex> lock(e->stage_mu);
+    const size_t head = L.cu + (size_t)(n_texts + 1) * 4;   // L.ids == 0
+    rc = e->stage.reserve(up256(head) + blob.size());
+    if (!rc) {
+      char* hb = e->stage.buf;
+      std::memcpy(hb + L.ids, ids_host, (size_t)n * 4);
+      rc = inl_positions_host(n_texts, cu, (int32_t*)(hb + L.pos));
+      std::memcpy(hb + L.cu, cu, (size_t)(n_texts + 1) * 4);
+      hipError_t err = rc ? hipSuccess : hipMemcpyAsync(ws, hb, head, hipMemcpyHostToDevice, st);
+      if (!rc && err == hipSuccess && !blob.empty()) {
+        std::memcpy(hb + up256(head), blob.data(), blob.size());
+        err = hipMemcpyAsync(ws + L.sched, hb + up256(head), blob.size(), hipMemcpyHostToDevice, st);
+      }
+      if (err != hipSuccess) rc = hip_fail(err, "qwen3: uploads");
+      if (!rc) rc = e->stage.record(st);
+    }
+  }
+  if (rc) {
+    (void)inl_attn_plan_destroy(plan);
+    return rc;
+  }
 
   // the launch sequence, onto stream `sq` (the caller's, or the capture stream)
   auto sequence = [&](void* sq) -> int {

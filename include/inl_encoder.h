@@ -171,7 +171,9 @@ int inl_qwen3_workspace_size(const inl_qwen3* enc, int32_t n_texts,
  * qwen3/mod.rs:468). ids_host: [cu_seqlens_host[n_texts]] token ids, checked
  * against vocab on the host. Texts of length 0 are refused, as the
  * reference refuses an empty tokenisation (qwen3/mod.rs:446-448).
- * The batch is uploaded with pageable copies on `stream`, then the layers
+ * The batch (ids, positions, offsets, the attention schedule) is uploaded
+ * on `stream` from the encoder's pinned staging buffer (held until those
+ * copies complete; it grows on the first call that needs more), then the layers
  * run. With graphs on (the default), the launch sequence of a batch shape -
  * the same device, cu_seqlens_host, workspace and embeddings pointer - is
  * captured on its second call and replayed from the third on (the first

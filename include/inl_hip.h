@@ -124,9 +124,10 @@ typedef struct inl_attn_plan inl_attn_plan;
 int inl_attn_plan_create(const inl_attn_desc* desc, inl_attn_plan** plan);
 /* The same plan with its schedule in the caller's device `workspace` (at
  * least inl_attn_workspace_size() bytes, 16-byte aligned), uploaded
- * asynchronously on `stream` from pageable host memory: nothing is allocated
- * on the device. The workspace must outlive the plan's launches; destroying
- * the plan does not free it. */
+ * asynchronously on `stream` from the plan's own host copy of the schedule,
+ * which lives until the plan is destroyed: nothing is allocated on the
+ * device. The workspace must outlive the plan's launches; destroying the
+ * plan does not free it. */
 int inl_attn_plan_create_in(const inl_attn_desc* desc, void* workspace,
                             size_t workspace_bytes, void* stream,
                             inl_attn_plan** plan);
