@@ -236,69 +236,124 @@ def e2e_cpu_baseline(weights, shape, ids, cu, seconds):
                        f"oracle/qwen3.py (numpy f32 forward: BLAS GEMMs, per-text attention), {spent:.2f} s")}
 
 
-def e2e_main(args):
-    """Configuration 1 end to end: the Qwen3-0.6B-architecture encoder on 8
-    texts of U[16, 256] tokens (778), embed -> 28 layers -> last-token pooling
-    -> L2, f32 or bf16; one step = one encode."""
+def qwen3_e2e_measure(torch, inl_hip, dev, bf16, steps, warmup, cpu_seconds, no_cpu):
+    """Configuration 1 end to end: the Qwen3-0.6B-architecture encoder on
+    batches of 8 texts of U[16, 256] tokens, embed -> 28 layers -> last-token
+    pooling -> L2, f32 or bf16.
+
+    Every timed step encodes a different draw of 8 texts (seeds 0..steps-1;
+    warm-up draws use other seeds), as an engine sees them: no two steps share
+    a batch shape, so no launch graph is ever replayed (graphs are off) and
+    each GEMM reuses its row-count bucket's algorithm choice instead of
+    tuning. For comparison, `repeated_batch` times draw 0 over and over with
+    the runner's launch graph on. Returns a dict (tokens/s, roofline, CPU
+    baseline)."""
     import numpy as np
-    import torch
-    import inl_hip
     from inl_hip import workloads as w
-    dev = torch.device("cuda:0")
-    bf16 = args.workload.endswith("bf16")
     td = torch.bfloat16 if bf16 else torch.float32
     shape = w.Qwen3Shape()
-    lengths = w.uniform_lengths(8, 16, 256)
-    cu = np.asarray(w.cu_seqlens(lengths))
-    ids = np.random.default_rng(0).integers(0, shape.vocab, int(cu[-1])).astype(np.int32)
+
+    def draw(seed):
+        lengths = w.uniform_lengths(8, 16, 256, seed=seed)
+        cu = w.cu_seqlens(lengths)
+        ids = np.random.default_rng(seed).integers(0, shape.vocab, cu[-1]).astype(np.int32)
+        return lengths, cu, ids
+
+    timed = [draw(s) for s in range(steps)]
+    warm = [draw(1000 + s) for s in range(max(warmup, 1))]
     weights = w.qwen3_random_weights(shape, torch, dev, td, seed=0)
     enc = inl_hip.Qwen3Encoder(shape, weights, max_positions=256)
-    out = torch.empty((len(lengths), shape.hidden), dtype=torch.float32, device=dev)
-    ws = torch.empty(enc.workspace_bytes(cu.tolist()) + 256, dtype=torch.uint8, device=dev)
+    out = torch.empty((8, shape.hidden), dtype=torch.float32, device=dev)
+    ws = torch.empty(max(enc.workspace_bytes(c) for _, c, _ in timed + warm) + 256, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
-    tokens = int(cu[-1])
     q_out, kv_out = shape.heads * shape.head_dim, shape.kv_heads * shape.head_dim
     per_token = 2 * (shape.hidden * (q_out + 2 * kv_out) + q_out * shape.hidden + 3 * shape.hidden * shape.intermediate)
-    flops = shape.layers * (tokens * per_token + inl_hip.attention_flops(lengths, shape.heads, shape.head_dim, True))
-    label = (f"config1: Qwen3-Embedding-0.6B-architecture encoder end to end ({'bf16' if bf16 else 'f32'}): 28 layers, "
-             f"hidden 1024, 16 Q / 8 KV heads x 128, RoPE theta 1e6, last-token pooling, L2; 8 texts U[16,256] "
-             f"= {tokens} tokens, random ids in [0,151669), random-init weights")
-    log(f"workload: {label}; {flops / 1e12:.4f} TFLOP per encode")
 
-    def step(evs=None):
-        if evs is not None:
-            evs[0][0].record(stream)
-        enc.encode(ids, cu.tolist(), out=out, workspace=ws, stream=stream)
-        if evs is not None:
-            evs[0][1].record(stream)
+    def flops_of(lengths):
+        return shape.layers * (sum(lengths) * per_token
+                               + inl_hip.attention_flops(lengths, shape.heads, shape.head_dim, True))
 
-    for _ in range(args.warmup):
-        step()
+    enc.set_graphs(False)
+    for _, cu, ids in warm:
+        enc.encode(ids, cu, out=out, workspace=ws, stream=stream)
     torch.cuda.synchronize()
+    tuned0 = inl_hip.linear_stats()["tunings"]
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for _, cu, ids in timed:
+        enc.encode(ids, cu, out=out, workspace=ws, stream=stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    avg_ms = timed_launches(torch, step, 1, args.steps)
+    tunings = inl_hip.linear_stats()["tunings"] - tuned0
+    # GPU time per encode from HIP events on the launch stream (same draws)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in timed]
+    for (a, b), (_, cu, ids) in zip(evs, timed):
+        a.record(stream)
+        enc.encode(ids, cu, out=out, workspace=ws, stream=stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    gpu_ms = sum(a.elapsed_time(b) for a, b in evs)
+    tokens = sum(c[-1] for _, c, _ in timed)
+    flops = sum(flops_of(l) for l, _, _ in timed)
+    # the same encoder on one repeated batch, launch graph on
+    enc.set_graphs(True)
+    _, cu0, ids0 = timed[0]
+    for _ in range(3):
+        enc.encode(ids0, cu0, out=out, workspace=ws, stream=stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        enc.encode(ids0, cu0, out=out, workspace=ws, stream=stream)
+    torch.cuda.synchronize()
+    rep_wall = time.perf_counter() - t1
     peak = PEAK_BF16_TFLOPS if bf16 else PEAK_F32_TFLOPS
-    ach = flops / (avg_ms * 1e-3) / 1e12
-    result = {
-        "metric": METRIC, "value": round(tokens * args.steps / wall, 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if bf16 else "f32",
-        "data": "synthetic (random token ids, seeded random-init weights; no checkpoint)",
-        "config": {"workload": label, "tokens_per_step": tokens, "texts": len(lengths),
-                   "tflop_per_step": round(flops / 1e12, 6),
-                   "value_is": "end-to-end encoded tokens/s (embed, 28 layers, pooling, L2 per step)"},
+    ach = flops / (gpu_ms * 1e-3) / 1e12
+    res = {
+        "metric": "encoded tokens/s", "value": round(tokens / wall, 1), "unit": "tokens/s",
+        "dtype": "bf16" if bf16 else "f32", "steps": steps, "warmup": len(warm),
+        "ms_per_step": round(wall / steps * 1e3, 4), "tokens": int(tokens),
+        "workload": (f"config1: Qwen3-Embedding-0.6B-architecture encoder end to end "
+                     f"({'bf16' if bf16 else 'f32'}): 28 layers, hidden 1024, 16 Q / 8 KV heads x 128, RoPE "
+                     f"theta 1e6, last-token pooling, L2; each step a new draw of 8 texts U[16,256] (seeds "
+                     f"0..{steps - 1}), random ids in [0,151669), random-init weights"),
+        "graphs": "off (every step is a new batch shape)",
+        "gemm_tunings_in_timed_steps": int(tunings),
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(ach / peak, 4), "traffic": None,
                      "kernel": "whole encode (hipBLASLt GEMMs, attention, prologue, norms, SwiGLU, pooling)",
-                     "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"flop": flops}},
+                     "avg_launch_us": round(gpu_ms / steps * 1e3, 2),
+                     "algorithmic_per_launch": {"flop": int(flops // steps)}},
+        "repeated_batch": {"value": round(cu0[-1] * steps / rep_wall, 1), "unit": "tokens/s",
+                           "ms_per_step": round(rep_wall / steps * 1e3, 4), "tokens_per_step": int(cu0[-1]),
+                           "graphs": "on (replayed from the third call)"},
     }
-    if not args.no_cpu:
-        result["cpu_baseline"] = e2e_cpu_baseline(weights, shape, ids, cu, args.cpu_seconds)
+    if not no_cpu:
+        l0, c0, i0 = timed[0]
+        res["cpu_baseline"] = e2e_cpu_baseline(weights, shape, i0, np.asarray(c0), cpu_seconds)
     enc.close()
+    return res
+
+
+def e2e_main(args):
+    """--workload qwen3_e2e (f32, configuration 1) or qwen3_e2e_bf16: the
+    configuration-1 measurement above as the line itself."""
+    import torch
+    import inl_hip
+    dev = torch.device("cuda:0")
+    bf16 = args.workload.endswith("bf16")
+    r = qwen3_e2e_measure(torch, inl_hip, dev, bf16, args.steps, args.warmup, args.cpu_seconds, args.no_cpu)
+    log(f"workload: {r['workload']}")
+    result = {
+        "metric": METRIC, "value": r["value"], "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": r["warmup"], "ms_per_step": r["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": r["dtype"],
+        "data": "synthetic (random token ids, seeded random-init weights; no checkpoint)",
+        "config": {"workload": r["workload"], "tokens_timed": r["tokens"], "graphs": r["graphs"],
+                   "gemm_tunings_in_timed_steps": r["gemm_tunings_in_timed_steps"],
+                   "value_is": "end-to-end encoded tokens/s (embed, 28 layers, pooling, L2 per step)"},
+        "roofline": r["roofline"], "repeated_batch": r["repeated_batch"],
+    }
+    if "cpu_baseline" in r:
+        result["cpu_baseline"] = r["cpu_baseline"]
     print(json.dumps(result), flush=True)
 
 
@@ -645,6 +700,8 @@ def main():
     ap.add_argument("--workload", default="qwen3")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="default workload only: skip the nested configuration-1 end-to-end measurement")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (3 launches): the known-size "
                          "reference that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -763,6 +820,13 @@ def main():
                                               args.cpu_seconds)
     for pl in plans:
         pl.close()
+    if args.workload == "qwen3" and not args.no_e2e:
+        # the metric's other half: configuration 1 encoded tokens/s end to end
+        del inputs, outs
+        torch.cuda.empty_cache()
+        result["e2e_config1"] = qwen3_e2e_measure(torch, inl_hip, dev, False, args.steps, args.warmup,
+                                                  args.cpu_seconds, args.no_cpu)
+        log(f"e2e config1: {result['e2e_config1']['value']} tokens/s")
     print(json.dumps(result), flush=True)
 
 

@@ -21,6 +21,17 @@
 // persistent: its tiles form one stream of stages, so the next tile's first
 // loads are in flight while the current tile's epilogue stores run.
 //
+// Gated epilogues (the GEGLU gates of EmbeddingGemma 2, gemma2.rs:249-254 and
+// :279-283, fused so that the gate and up products never reach memory):
+//   - GEGLU: w holds gate rows [0, n) then up rows [n, 2n) (the stacked
+//     gate/up projection); y[m, c] = gelu_tanh(x . gate_c) * (x . up_c). A
+//     tile covers 128 output columns and reads 128 gate and 128 up rows,
+//     ordered in its LDS as alternating 16-row chunks, so each 32-row MFMA
+//     block is 16 gate rows then the 16 matching up rows and a lane holds
+//     both factors of its outputs;
+//   - GELU x multiplier: y[m, c] = gelu_tanh(x . w_c) * mul[m, c].
+// gelu_tanh(v) = v / 2 * (1 + tanh(sqrt(2 / pi) * (v + 0.044715 v^3))) in f32.
+//
 // Tile order: workgroup b runs on XCD b % 8. The tiles, m-tile major (all
 // n-tiles of one 256-row block of x in a row), are cut into 8 contiguous
 // ranges, one per XCD, and each XCD's workgroups take every 32nd tile of its
@@ -53,10 +64,14 @@ constexpr int GM_XCDS = 8;
 static_assert(GM_BLOCKS % GM_NW == 0, "the direct loads split evenly over the waves");
 static_assert(GM_PER_WAVE % 2 == 0, "each wave loads w blocks then x blocks");
 
+enum GemmEpi { EPI_PLAIN = 0, EPI_GEGLU = 1, EPI_GELU_MUL = 2 };
+
 struct GemmParams {
   const char* x;
   const char* w;
   char* y;
+  const char* mul;          // EPI_GELU_MUL: bf16 [m, n] rows of ms elements
+  int64_t ms;
   int64_t m;
   int32_t n, k;
   int64_t xs_b, ws_b, ys;   // x and w row strides in bytes, y row stride in elements
@@ -71,8 +86,14 @@ struct GemmParams {
 // the 16 rows one ds_read_b128 pass touches then cover all 64 banks.
 __device__ __forceinline__ uint32_t gm_swz(int r, int c) { return r * GM_ROW + ((c ^ ((r >> 2) & 3)) << 4); }
 
-template <bool OUT_BF16, bool ACC>
+__device__ __forceinline__ float gelu_tanh(float v) {
+  return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+}
+
+template <int EPI, bool OUT_BF16, bool ACC>
 __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
+  // output columns per tile: a GEGLU tile's 256 w rows are 128 gate + 128 up
+  constexpr int BNO = EPI == EPI_GEGLU ? GM_BN / 2 : GM_BN;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int xcd = blockIdx.x % GM_XCDS;
   const int slot = blockIdx.x / GM_XCDS;
@@ -100,7 +121,9 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
     const int r = lane >> 2, cp = lane & 3;
     const int c = cp ^ ((r >> 2) & 3);
     const bool is_w = i < GM_PER_WAVE / 2;
-    const int row = (is_w ? blk : blk - GM_W / 1024) * 16 + r;
+    // GEGLU: w block blk is 16-row chunk blk / 2 of the gate rows (blk even)
+    // or of the up rows (blk odd); every w block of a wave has the wave's parity
+    const int row = (is_w ? (EPI == EPI_GEGLU ? blk >> 1 : blk) : blk - GM_W / 1024) * 16 + r;
     goff[i] = (uint32_t)row * (uint32_t)(is_w ? p.ws_b : p.xs_b) + c * 16;
   }
   // The descriptors of a tile start at its first x row / w row, so no offset
@@ -118,13 +141,16 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
     const int64_t rows = min((int64_t)GM_BM, p.m - r0);
     return pp_rsrc_words(p.x + r0 * p.xs_b, (uint32_t)(rows * p.xs_b));
   };
+  // this wave's w descriptor: the tile's w rows, or (GEGLU) its gate rows
+  // (even waves) or up rows (odd waves)
   auto rsrc_w = [&](int j) __attribute__((always_inline)) {
     int64_t mt;
     int nt;
     tile_of(j, &mt, &nt);
-    const int r0 = nt * GM_BN;
-    const int rows = min(GM_BN, p.n - r0);
-    return pp_rsrc_words(p.w + (int64_t)r0 * p.ws_b, (uint32_t)((int64_t)rows * p.ws_b));
+    const int r0 = nt * BNO;
+    const int rows = min(BNO, p.n - r0);
+    const int64_t first = EPI == EPI_GEGLU && (wave & 1) ? (int64_t)p.n + r0 : (int64_t)r0;
+    return pp_rsrc_words(p.w + first * p.ws_b, (uint32_t)((int64_t)rows * p.ws_b));
   };
   const i32x4 none = pp_rsrc_words(p.x, 0);   // loads past the last stage read zeros
 
@@ -190,9 +216,9 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
         acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, f.a[a]),
                                                             __builtin_bit_cast(bf16x8, f.b[b]), acc[a][b], 0, 0, 0);
   };
-  // tile done: acc[a][b][4 * g + e] is output (row wm*64 + b*32 + l32,
-  // column wn*128 + a*32 + 8*g + 4*hf + e) of the tile
   int mm_j = 0, mm_ks = 0;   // the MFMA cursor
+  // tile done: acc[a][b][4 * g + e] is product (row wm*64 + b*32 + l32,
+  // w row wn*128 + a*32 + 8*g + 4*hf + e) of the tile
   auto tile_end = [&]() __attribute__((always_inline)) {
     if (++mm_ks != kst) return;
     mm_ks = 0;
@@ -200,43 +226,70 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
     int nt;
     tile_of(mm_j++, &mt, &nt);
     const int64_t row0 = mt * GM_BM + wm * 64 + l32;
-    const int col0 = nt * GM_BN + wn * 128 + 4 * hf;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int64_t row = row0 + b * 32;
       if (row < p.m) {
         char* yr = p.y + row * p.ys * (OUT_BF16 ? 2 : 4);
+        auto put = [&](int col, f32x4 v) __attribute__((always_inline)) {
+          if constexpr (OUT_BF16) {
+            bf16x4* dst = reinterpret_cast<bf16x4*>(yr + (int64_t)col * 2);
+            if constexpr (ACC) {
+              const bf16x4 o = *dst;
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+              for (int e = 0; e < 4; ++e) v[e] += p.beta * (float)o[e];
+            }
+            bf16x4 r;
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int col = col0 + a * 32 + 8 * g;
-            if (col < p.n) {
-              f32x4 v;
+            for (int e = 0; e < 4; ++e) r[e] = (bf16)v[e];
+            *dst = r;
+          } else {
+            f32x4* dst = reinterpret_cast<f32x4*>(yr + (int64_t)col * 4);
+            if constexpr (ACC) {
+              const f32x4 o = *dst;
 #pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[a][b][4 * g + e];
-              if constexpr (OUT_BF16) {
-                bf16x4* dst = reinterpret_cast<bf16x4*>(yr + (int64_t)col * 2);
-                if constexpr (ACC) {
-                  const bf16x4 o = *dst;
+              for (int e = 0; e < 4; ++e) v[e] += p.beta * o[e];
+            }
+            *dst = v;
+          }
+        };
 #pragma unroll
-                  for (int e = 0; e < 4; ++e) v[e] += p.beta * (float)o[e];
+        for (int a = 0; a < 4; ++a) {
+          if constexpr (EPI == EPI_GEGLU) {
+            // MFMA block wn*4 + a: gate rows 0-15 of the block and their up
+            // rows 16-31, output columns 16 * (wn*4 + a) + 0..15 of the tile
+            const int colb = nt * BNO + (wn * 4 + a) * 16 + 4 * hf;
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+              const int col = colb + 8 * g;
+              if (col < p.n) {
+                f32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  v[e] = gelu_tanh(p.alpha * acc[a][b][4 * g + e]) * (p.alpha * acc[a][b][4 * (g + 2) + e]);
+                put(col, v);
+              }
+            }
+          } else {
+            const int colb = nt * BNO + wn * 128 + a * 32 + 4 * hf;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int col = colb + 8 * g;
+              if (col < p.n) {
+                f32x4 v;
+                if constexpr (EPI == EPI_GELU_MUL) {
+                  const bf16x4 mv = *reinterpret_cast<const bf16x4*>(p.mul + (row * p.ms + col) * 2);
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(p.alpha * acc[a][b][4 * g + e]) * (float)mv[e];
+                } else {
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[a][b][4 * g + e];
                 }
-                bf16x4 r;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) r[e] = (bf16)v[e];
-                *dst = r;
-              } else {
-                f32x4* dst = reinterpret_cast<f32x4*>(yr + (int64_t)col * 4);
-                if constexpr (ACC) {
-                  const f32x4 o = *dst;
-#pragma unroll
-                  for (int e = 0; e < 4; ++e) v[e] += p.beta * o[e];
-                }
-                *dst = v;
+                put(col, v);
               }
             }
           }
+        }
       }
     }
 #pragma unroll
@@ -272,9 +325,82 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the dummy loads past the end
 }
 
-template <bool B, bool A>
+template <int E, bool B, bool A>
 const void* gemm_fn() {
-  return (const void*)gemm_bf16_kernel<B, A>;
+  return (const void*)gemm_bf16_kernel<E, B, A>;
+}
+
+// Launch for every epilogue; `n` is the output width (GEGLU: w has 2n rows).
+int gemm_launch(int epi, int64_t m, int64_t n, int64_t k, const void* x, int64_t x_stride, const void* w,
+                int64_t w_stride, const void* mul, int64_t mul_stride, int32_t out_dtype, void* y, int64_t y_stride,
+                float alpha, float beta, void* stream) {
+  if (m < 0 || n <= 0 || k <= 0) return fail(INL_E_INVALID, "gemm: m must be >= 0, n and k > 0");
+  if (!dtype_ok(out_dtype)) return fail(INL_E_INVALID, "gemm: out_dtype must be f32 or bf16");
+  if (k % GM_BK || n % 8)
+    return fail(INL_E_UNSUPPORTED, "gemm: k must be a multiple of 32 and n a multiple of 8");
+  if (n > (1 << 29) || k > (1 << 20)) return fail(INL_E_UNSUPPORTED, "gemm: n or k too large");
+  const int64_t xs = x_stride ? x_stride : k, ws = w_stride ? w_stride : k, ys = y_stride ? y_stride : n;
+  const int64_t ms = mul_stride ? mul_stride : n;
+  if (xs < k || ws < k || ys < n || (epi == EPI_GELU_MUL && ms < n))
+    return fail(INL_E_INVALID, "gemm: a row stride is shorter than its row");
+  if (xs % 8 || ws % 8 || ys % 8 || (epi == EPI_GELU_MUL && ms % 4))
+    return fail(INL_E_UNSUPPORTED, "gemm: row strides must be multiples of 8 elements (the multiplier's of 4)");
+  if (m == 0) return INL_OK;
+  if (!x || !w || !y || (epi == EPI_GELU_MUL && !mul)) return fail(INL_E_INVALID, "gemm: NULL x, w, y or multiplier");
+  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)y & 15) || ((uintptr_t)mul & 7))
+    return fail(INL_E_INVALID, "gemm: x, w and y must be 16-byte aligned, the multiplier 8-byte aligned");
+  // each tile's descriptor spans at most 256 rows of x or w
+  if ((int64_t)GM_BM * xs * 2 >= ((int64_t)1 << 32) || (int64_t)GM_BN * ws * 2 >= ((int64_t)1 << 32))
+    return fail(INL_E_UNSUPPORTED, "gemm: row strides too large for a tile's 32-bit buffer range");
+  int dev = 0, cus = 0;
+  INL_HIP_TRY(hipGetDevice(&dev));
+  INL_HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const int bno = epi == EPI_GEGLU ? GM_BN / 2 : GM_BN;
+  GemmParams p{};
+  p.x = (const char*)x;
+  p.w = (const char*)w;
+  p.y = (char*)y;
+  p.mul = (const char*)mul;
+  p.ms = ms;
+  p.m = m;
+  p.n = (int32_t)n;
+  p.k = (int32_t)k;
+  p.xs_b = xs * 2;
+  p.ws_b = ws * 2;
+  p.ys = ys;
+  p.alpha = alpha;
+  p.beta = beta;
+  p.n_tiles_n = (int32_t)((n + bno - 1) / bno);
+  p.n_tiles = ((m + GM_BM - 1) / GM_BM) * p.n_tiles_n;
+  p.per_xcd = (p.n_tiles + GM_XCDS - 1) / GM_XCDS;
+  // one workgroup per CU (96 KiB of LDS each), at most one per tile of an XCD's range
+  const int64_t per_xcd_wg = std::max<int64_t>(1, std::min<int64_t>(cus / GM_XCDS, p.per_xcd));
+  p.wg_per_xcd = (int32_t)per_xcd_wg;
+  if ((int64_t)(p.per_xcd + per_xcd_wg - 1) / per_xcd_wg * (k / GM_BK) >= ((int64_t)1 << 31))
+    return fail(INL_E_UNSUPPORTED, "gemm: too many k stages per workgroup");
+  const bool bf = out_dtype == INL_BF16, acc = beta != 0.f;
+  const void* fn = nullptr;
+  switch (epi * 4 + (bf ? 2 : 0) + (acc ? 1 : 0)) {
+#define INL_GEMM_CASE(E, B, A) \
+  case E * 4 + (B ? 2 : 0) + (A ? 1 : 0): fn = gemm_fn<E, B, A>(); break;
+    INL_GEMM_CASE(EPI_PLAIN, false, false)
+    INL_GEMM_CASE(EPI_PLAIN, false, true)
+    INL_GEMM_CASE(EPI_PLAIN, true, false)
+    INL_GEMM_CASE(EPI_PLAIN, true, true)
+    INL_GEMM_CASE(EPI_GEGLU, false, false)
+    INL_GEMM_CASE(EPI_GEGLU, true, false)
+    INL_GEMM_CASE(EPI_GELU_MUL, false, false)
+    INL_GEMM_CASE(EPI_GELU_MUL, true, false)
+#undef INL_GEMM_CASE
+    default:
+      return fail(INL_E_UNSUPPORTED, "gemm: the gated epilogues take beta = 0");
+  }
+  int rc = set_max_dynamic_lds(fn, GM_LDS);
+  if (rc) return rc;
+  void* args[] = {&p};
+  INL_HIP_TRY(hipLaunchKernel(fn, dim3((unsigned)(per_xcd_wg * GM_XCDS)), dim3(GM_NW * 64), args, GM_LDS,
+                              (hipStream_t)stream));
+  return INL_OK;
 }
 
 }  // namespace
@@ -284,59 +410,17 @@ const void* gemm_fn() {
 extern "C" int inl_gemm_bf16_fwd(int64_t m, int64_t n, int64_t k, const void* x, int64_t x_stride, const void* w,
                                  int64_t w_stride, int32_t out_dtype, void* y, int64_t y_stride, float alpha,
                                  float beta, void* stream) {
+  return inl::gemm_launch(inl::EPI_PLAIN, m, n, k, x, x_stride, w, w_stride, nullptr, 0, out_dtype, y, y_stride,
+                          alpha, beta, stream);
+}
+
+extern "C" int inl_gemm_bf16_gated_fwd(int64_t m, int64_t n, int64_t k, const void* x, int64_t x_stride,
+                                       const void* w, int64_t w_stride, int32_t mode, const void* mul,
+                                       int64_t mul_stride, int32_t out_dtype, void* y, int64_t y_stride,
+                                       void* stream) {
   using namespace inl;
-  if (m < 0 || n <= 0 || k <= 0) return fail(INL_E_INVALID, "gemm: m must be >= 0, n and k > 0");
-  if (!dtype_ok(out_dtype)) return fail(INL_E_INVALID, "gemm: out_dtype must be f32 or bf16");
-  if (k % GM_BK || n % 8)
-    return fail(INL_E_UNSUPPORTED, "gemm: k must be a multiple of 32 and n a multiple of 8");
-  if (n > (1 << 30) || k > (1 << 20)) return fail(INL_E_UNSUPPORTED, "gemm: n or k too large");
-  const int64_t xs = x_stride ? x_stride : k, ws = w_stride ? w_stride : k, ys = y_stride ? y_stride : n;
-  if (xs < k || ws < k || ys < n) return fail(INL_E_INVALID, "gemm: a row stride is shorter than its row");
-  if (xs % 8 || ws % 8 || ys % 8) return fail(INL_E_UNSUPPORTED, "gemm: row strides must be multiples of 8 elements");
-  if (m == 0) return INL_OK;
-  if (!x || !w || !y) return fail(INL_E_INVALID, "gemm: NULL x, w or y");
-  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)y & 15))
-    return fail(INL_E_INVALID, "gemm: x, w and y must be 16-byte aligned");
-  // each tile's descriptor spans at most 256 rows of x or w
-  if ((int64_t)GM_BM * xs * 2 >= ((int64_t)1 << 32) || (int64_t)GM_BN * ws * 2 >= ((int64_t)1 << 32))
-    return fail(INL_E_UNSUPPORTED, "gemm: row strides too large for a tile's 32-bit buffer range");
-  int dev = 0, cus = 0;
-  INL_HIP_TRY(hipGetDevice(&dev));
-  INL_HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  GemmParams p{};
-  p.x = (const char*)x;
-  p.w = (const char*)w;
-  p.y = (char*)y;
-  p.m = m;
-  p.n = (int32_t)n;
-  p.k = (int32_t)k;
-  p.xs_b = xs * 2;
-  p.ws_b = ws * 2;
-  p.ys = ys;
-  p.alpha = alpha;
-  p.beta = beta;
-  p.n_tiles_n = (int32_t)((n + GM_BN - 1) / GM_BN);
-  p.n_tiles = ((m + GM_BM - 1) / GM_BM) * p.n_tiles_n;
-  p.per_xcd = (p.n_tiles + GM_XCDS - 1) / GM_XCDS;
-  // one workgroup per CU (96 KiB of LDS each), at most one per tile of an XCD's range
-  const int64_t per_xcd_wg = std::max<int64_t>(1, std::min<int64_t>(cus / GM_XCDS, p.per_xcd));
-  p.wg_per_xcd = (int32_t)per_xcd_wg;
-  if ((int64_t)(p.per_xcd + per_xcd_wg - 1) / per_xcd_wg * (k / GM_BK) >= ((int64_t)1 << 31))
-    return fail(INL_E_UNSUPPORTED, "gemm: too many k stages per workgroup");
-  const bool bf = out_dtype == INL_BF16, acc = beta != 0.f;
-  const void* fn = bf ? (acc ? gemm_fn<true, true>() : gemm_fn<true, false>())
-                      : (acc ? gemm_fn<false, true>() : gemm_fn<false, false>());
-  int rc = set_max_dynamic_lds(fn, GM_LDS);
-  if (rc) return rc;
-  const dim3 grid((unsigned)(per_xcd_wg * GM_XCDS)), block(GM_NW * 64);
-  hipStream_t st = (hipStream_t)stream;
-  if (bf) {
-    if (acc) hipLaunchKernelGGL((gemm_bf16_kernel<true, true>), grid, block, GM_LDS, st, p);
-    else hipLaunchKernelGGL((gemm_bf16_kernel<true, false>), grid, block, GM_LDS, st, p);
-  } else {
-    if (acc) hipLaunchKernelGGL((gemm_bf16_kernel<false, true>), grid, block, GM_LDS, st, p);
-    else hipLaunchKernelGGL((gemm_bf16_kernel<false, false>), grid, block, GM_LDS, st, p);
-  }
-  INL_HIP_TRY(hipGetLastError());
-  return INL_OK;
+  if (mode != INL_GATE_GEGLU && mode != INL_GATE_GELU_MUL)
+    return fail(INL_E_INVALID, "gemm: mode must be INL_GATE_GEGLU or INL_GATE_GELU_MUL");
+  return gemm_launch(mode == INL_GATE_GEGLU ? EPI_GEGLU : EPI_GELU_MUL, m, n, k, x, x_stride, w, w_stride, mul,
+                     mul_stride, out_dtype, y, y_stride, 1.f, 0.f, stream);
 }

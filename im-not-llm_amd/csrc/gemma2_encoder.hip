@@ -584,12 +584,22 @@ extern "C" int inl_gemma2_encode(inl_gemma2* e, int32_t n_texts, const int32_t* 
     if (!rc) rc = gemm(dt, n, H, qd, B, L.b_w, w.o_proj, qd, INL_F32, T, H, 1.f, gws, gws_bytes, stream);
     if (!rc) rc = launch_post_add(dt, n, c.hidden, h, T, w.post_attention_norm, nullptr, c.eps, w.pre_feedforward_norm,
                                   x, st);
-    if (!rc) rc = gemm(dt, n, 2 * I, H, x, H, w.gate_up_proj, H, dt, A, L.a_w, 1.f, gws, gws_bytes, stream);
-    if (!rc) rc = launch_gelu_gate(dt, n, c.intermediate, A, L.a_w, A + I * es, L.a_w, B, L.b_w, st);
+    // m = gelu_tanh(x . Wgate^T) * (x . Wup^T): one fused GEMM in bf16
+    if (!rc && dt == INL_BF16 && own_gemm_ok(I, H, H, H, L.b_w)) {
+      rc = inl_gemm_bf16_gated_fwd(n, I, H, x, H, w.gate_up_proj, H, INL_GATE_GEGLU, nullptr, 0, dt, B, L.b_w, stream);
+    } else {
+      if (!rc) rc = gemm(dt, n, 2 * I, H, x, H, w.gate_up_proj, H, dt, A, L.a_w, 1.f, gws, gws_bytes, stream);
+      if (!rc) rc = launch_gelu_gate(dt, n, c.intermediate, A, L.a_w, A + I * es, L.a_w, B, L.b_w, st);
+    }
     if (!rc) rc = gemm(dt, n, H, I, B, L.b_w, w.down_proj, I, INL_F32, T, H, 1.f, gws, gws_bytes, stream);
     if (!rc) rc = launch_post_add(dt, n, c.hidden, h, T, w.post_feedforward_norm, nullptr, c.eps, nullptr, x, st);
-    if (!rc) rc = gemm(dt, n, E, H, x, H, w.ple_input_gate, H, dt, A, L.a_w, 1.f, gws, gws_bytes, stream);
-    if (!rc) rc = launch_gelu_gate(dt, n, c.ple_dim, A, L.a_w, P, E, B, L.b_w, st);
+    // g = gelu_tanh(h . Wgate_ple^T) * per_layer: one fused GEMM in bf16
+    if (!rc && dt == INL_BF16 && own_gemm_ok(E, H, H, H, L.b_w) && E % 4 == 0) {
+      rc = inl_gemm_bf16_gated_fwd(n, E, H, x, H, w.ple_input_gate, H, INL_GATE_GELU_MUL, P, E, dt, B, L.b_w, stream);
+    } else {
+      if (!rc) rc = gemm(dt, n, E, H, x, H, w.ple_input_gate, H, dt, A, L.a_w, 1.f, gws, gws_bytes, stream);
+      if (!rc) rc = launch_gelu_gate(dt, n, c.ple_dim, A, L.a_w, P, E, B, L.b_w, st);
+    }
     if (!rc) rc = gemm(dt, n, H, E, B, L.b_w, w.ple_projection, E, INL_F32, T, H, 1.f, gws, gws_bytes, stream);
     const void* next_norm = i + 1 < c.layers ? e->layers[i + 1].input_norm : e->final_norm;
     if (!rc) rc = launch_post_add(dt, n, c.hidden, h, T, w.ple_post_norm, w.layer_scalar, c.eps, next_norm, x, st);

@@ -517,6 +517,9 @@ _linear = _sig("inl_linear_fwd", ctypes.c_int, c_i64, c_i64, c_i64, c_i32, c_voi
                c_i32, c_void_p, c_i64, ctypes.c_float, ctypes.c_float, c_void_p, ctypes.c_size_t, c_void_p)
 _gemm = _sig("inl_gemm_bf16_fwd", ctypes.c_int, c_i64, c_i64, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i32,
              c_void_p, c_i64, ctypes.c_float, ctypes.c_float, c_void_p)
+_gemm_gated = _sig("inl_gemm_bf16_gated_fwd", ctypes.c_int, c_i64, c_i64, c_i64, c_void_p, c_i64, c_void_p, c_i64,
+                   c_i32, c_void_p, c_i64, c_i32, c_void_p, c_i64, c_void_p)
+INL_GATE_GEGLU, INL_GATE_GELU_MUL = 1, 2
 _embed = _sig("inl_embed_fwd", ctypes.c_int, c_i64, c_void_p, c_void_p, c_i64, c_i32, c_i32, c_void_p, c_i64,
               c_void_p)
 _rms_rows = _sig("inl_rms_norm_rows_fwd", ctypes.c_int, c_i64, c_i32, c_void_p, c_i64, c_void_p, c_i32,
@@ -598,6 +601,37 @@ def gemm_bf16(x, w, *, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=Non
         raise InlError(-1, f"gemm_bf16: out must be [{m}, {n}] with contiguous rows")
     _check(_gemm(m, n, k, x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), _dtype_code(out.dtype),
                  out.data_ptr(), out.stride(0), float(alpha), float(beta), _stream_ptr(stream)))
+    return out
+
+
+def gemm_bf16_gated(x, w, mode, *, mul=None, out=None, out_dtype=None, stream=None):
+    """``inl_gemm_bf16_gated_fwd``: ``mode="geglu"``: ``w [2n, k]`` (gate rows
+    then up rows), ``out = gelu_tanh(x @ w[:n].T) * (x @ w[n:].T)``;
+    ``mode="gelu_mul"``: ``out = gelu_tanh(x @ w.T) * mul`` (bf16 ``[m, n]``)."""
+    import torch
+    m, k = x.shape
+    if mode == "geglu":
+        code, n = INL_GATE_GEGLU, w.shape[0] // 2
+        if w.shape[0] % 2:
+            raise InlError(-1, "gemm_bf16_gated: geglu needs an even number of w rows")
+    elif mode == "gelu_mul":
+        code, n = INL_GATE_GELU_MUL, w.shape[0]
+        if mul is None or mul.shape != (m, n) or mul.dtype != torch.bfloat16 or mul.stride(1) != 1:
+            raise InlError(-1, f"gemm_bf16_gated: gelu_mul needs a bf16 mul [{m}, {n}] with contiguous rows")
+    else:
+        raise InlError(-1, f"gemm_bf16_gated: unknown mode {mode!r}")
+    if w.shape[1] != k or x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise InlError(-1, "gemm_bf16_gated: x and w must be bf16 and agree in k")
+    if x.stride(1) != 1 or w.stride(1) != 1:
+        raise InlError(-1, "gemm_bf16_gated: rows must be contiguous")
+    od = out_dtype if out_dtype is not None else (out.dtype if out is not None else torch.bfloat16)
+    if out is None:
+        out = torch.empty((m, n), dtype=od, device=x.device)
+    if out.shape != (m, n) or out.stride(1) != 1:
+        raise InlError(-1, f"gemm_bf16_gated: out must be [{m}, {n}] with contiguous rows")
+    _check(_gemm_gated(m, n, k, x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), code,
+                       mul.data_ptr() if mul is not None else None, mul.stride(0) if mul is not None else 0,
+                       _dtype_code(out.dtype), out.data_ptr(), out.stride(0), _stream_ptr(stream)))
     return out
 
 

@@ -67,6 +67,25 @@ int inl_gemm_bf16_fwd(int64_t m, int64_t n, int64_t k, const void* x,
                       int32_t out_dtype, void* y, int64_t y_stride,
                       float alpha, float beta, void* stream);
 
+/* The same GEMM with a gated epilogue, for the GEGLU gates of EmbeddingGemma
+ * 2 (crates/inl-text/src/gemma2.rs:249-254 Mlp::forward, :279-283 the
+ * per-layer-input gate), gelu_tanh(v) = v/2 (1 + tanh(sqrt(2/pi)(v + 0.044715
+ * v^3))) in f32 on the f32 products:
+ *   INL_GATE_GEGLU:    w [2n, k] = gate rows then up rows (the stacked
+ *                      gate/up projection);
+ *                      y[m, c] = gelu_tanh(x . w[c]) * (x . w[n + c])
+ *   INL_GATE_GELU_MUL: w [n, k]; mul [m, n] bf16 rows of mul_stride;
+ *                      y[m, c] = gelu_tanh(x . w[c]) * mul[m, c]
+ * The gate and up products never reach memory. Limits as inl_gemm_bf16_fwd
+ * (mul 8-byte aligned, mul_stride a multiple of 4). */
+#define INL_GATE_GEGLU 1
+#define INL_GATE_GELU_MUL 2
+int inl_gemm_bf16_gated_fwd(int64_t m, int64_t n, int64_t k, const void* x,
+                            int64_t x_stride, const void* w, int64_t w_stride,
+                            int32_t mode, const void* mul, int64_t mul_stride,
+                            int32_t out_dtype, void* y, int64_t y_stride,
+                            void* stream);
+
 /* out[t, :] = f32(table[ids[t], :]): the token embedding (candle Embedding,
  * qwen3/mod.rs:322-323,350) into an f32 residual stream. ids are device
  * int32; an id outside [0, vocab) yields a NaN row (check ids first). */

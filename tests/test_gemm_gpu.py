@@ -128,3 +128,61 @@ def test_gemm_config3_shapes(n, k, xs, ys, out, cuda, inl):
     # tile left at zero would move the sums by ~1e-2; unwritten elements stay
     # NaN and fail above.
     assert rel <= (1e-4 if out == "f32" else 5e-3), rel
+
+
+def _gelu_tanh(v):
+    return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v ** 3)))
+
+
+@pytest.mark.parametrize("mode,m,n,k", [("geglu", 300, 200, 64), ("geglu", 3001, 1152, 768),
+                                        ("gelu_mul", 257, 264, 96), ("gelu_mul", 3001, 256, 768)])
+def test_gated_gemm_against_fp64(mode, m, n, k, cuda, inl):
+    """The fused GEGLU and GELU x multiplier epilogues against the f64
+    product of the same bf16 values, gelu_tanh in f64: within the bf16
+    output rounding (2^-8 relative) plus 1e-5 of the largest |y| (the f32
+    accumulation and f32 tanh)."""
+    import torch
+    x = _rand(torch, cuda, (m, k), 7)
+    w = _rand(torch, cuda, (2 * n if mode == "geglu" else n, k), 8, k ** -0.5)
+    mul = _rand(torch, cuda, (m, n), 9) if mode == "gelu_mul" else None
+    print(f"case=gated gemm {mode} m={m} n={n} k={k}", flush=True)
+    y = inl.gemm_bf16_gated(x, w, mode, mul=mul)
+    xd, wd = x.double().cpu().numpy(), w.double().cpu().numpy()
+    if mode == "geglu":
+        ref = _gelu_tanh(xd @ wd[:n].T) * (xd @ wd[n:].T)
+    else:
+        ref = _gelu_tanh(xd @ wd.T) * mul.double().cpu().numpy()
+    got = y.double().cpu().numpy()
+    tol = 2.0 ** -8 * np.abs(ref) + 1e-5 * np.abs(ref).max()
+    assert (np.abs(got - ref) <= tol).all(), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("mode", ["geglu", "gelu_mul"])
+def test_gated_gemm_config3_full_size(mode, cuda, inl):
+    """Configuration 3's two gates at 139,124 rows (MLP: gate/up 2 x 1152
+    rows of 768, output rows of 1152; per-layer input: 256 columns times the
+    per-layer input rows): no row left unwritten, sampled rows within the
+    bound above."""
+    import torch
+    m, k = 139124, 768
+    n = 1152 if mode == "geglu" else 256
+    x = _rand(torch, cuda, (m, k), 10)
+    w = _rand(torch, cuda, (2 * n if mode == "geglu" else n, k), 11, k ** -0.5)
+    mul = _rand(torch, cuda, (m, n), 12) if mode == "gelu_mul" else None
+    y = torch.full((m, 1152), float("nan"), dtype=torch.bfloat16, device=cuda)
+    print(f"case=gated gemm {mode} config3 full size", flush=True)
+    inl.gemm_bf16_gated(x, w, mode, mul=mul, out=y[:, :n])
+    torch.cuda.synchronize()
+    assert not torch.isnan(y[:, :n]).any().item()
+    if n < 1152:
+        assert torch.isnan(y[:, n:]).all().item()
+    rows = np.unique(np.concatenate([[0, 1, 255, 256, m - 1], np.random.default_rng(1).integers(0, m, 300)]))
+    ri = torch.from_numpy(rows).to(cuda)
+    xd, wd = x[ri].double().cpu().numpy(), w.double().cpu().numpy()
+    if mode == "geglu":
+        ref = _gelu_tanh(xd @ wd[:n].T) * (xd @ wd[n:].T)
+    else:
+        ref = _gelu_tanh(xd @ wd.T) * mul[ri].double().cpu().numpy()
+    got = y[ri, :n].double().cpu().numpy()
+    tol = 2.0 ** -8 * np.abs(ref) + 1e-5 * np.abs(ref).max()
+    assert (np.abs(got - ref) <= tol).all(), np.abs(got - ref).max()
