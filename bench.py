@@ -197,13 +197,13 @@ def roofline(tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch, pe
                       "frac": round(gbs / PEAK_HBM_GBS, 4)}}
 
 
-OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade", "splade_decoder", "gdn_conv", "gdn_rule",
+OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade", "splade_decoder", "gemm", "gdn_conv", "gdn_rule",
                 "gdn_gated_norm")
 # What bounds each op workload that is not HBM-bound: the decoder is a GEMM
 # on the bf16 matrix cores; the delta rule is f32 vector (VALU) work, graded
 # against MI355X's 157.3 TFLOP/s fp32 vector peak (which counts packed-fp32
 # FMAs; this build disables packed fp32, so 78.6 TFLOP/s is its ceiling).
-OP_BOUND = {"splade_decoder": "mfma", "gdn_rule": "valu"}
+OP_BOUND = {"splade_decoder": "mfma", "gemm": "mfma", "gdn_rule": "valu"}
 E2E_WORKLOADS = ("qwen3_e2e", "qwen3_e2e_bf16")
 PEAK_F32_TFLOPS = 157.3     # MI355X fp32 peak: dense matrix, and vector with packed FMAs
 
@@ -579,6 +579,37 @@ def op_workload(name, torch, inl_hip, dev):
         label = (f"config4 SPLADE epilogue: max over {S} speaking rows x {V} f32 logits of 128 texts "
                  f"U[32,2048], finish (shift 10), fold to {terms} terms")
         return label, "splade_kernel", 1, timed(launches), S, nbytes, "f32"
+    if name == "gemm":
+        # config 3: one layer's projections on the hand-written bf16 GEMM at
+        # 139,124 tokens, as the EmbeddingGemma 2 runner issues them
+        # (q/k/v rows of 2304, the fused GEGLU and per-layer-input gates)
+        import numpy as np
+        m, H, I, E = 139124, 768, 1152, 256
+        x = torch.randn(m, H, generator=g, device=dev).to(torch.bfloat16)
+        xb = torch.randn(m, I, generator=g, device=dev).to(torch.bfloat16)
+        A = torch.empty(m, 2304, device=dev, dtype=torch.bfloat16)
+        B = torch.empty(m, I, device=dev, dtype=torch.bfloat16)
+        T = torch.empty(m, H, device=dev)
+        Tp = torch.empty(m, E, device=dev)
+        P = torch.randn(m, E, generator=g, device=dev).to(torch.bfloat16)
+        wt = lambda r, c: (torch.randn(r, c, generator=g, device=dev) * c ** -0.5).to(torch.bfloat16)
+        w_ple, w_qkv, w_o, w_gu, w_d, w_g, w_p = wt(E, H), wt(1280, H), wt(H, 768), wt(2 * I, H), wt(H, I), \
+            wt(E, H), wt(H, E)
+        launches = [
+            lambda: inl_hip.gemm_bf16(x, w_ple, out=Tp, alpha=H ** -0.5, stream=stream),
+            lambda: inl_hip.gemm_bf16(x, w_qkv, out=A[:, :1280], stream=stream),
+            lambda: inl_hip.gemm_bf16(xb[:, :768], w_o, out=T, stream=stream),
+            lambda: inl_hip.gemm_bf16_gated(x, w_gu, "geglu", out=B, stream=stream),
+            lambda: inl_hip.gemm_bf16(xb, w_d, out=T, stream=stream),
+            lambda: inl_hip.gemm_bf16_gated(x, w_g, "gelu_mul", mul=P, out=B[:, :E], stream=stream),
+            lambda: inl_hip.gemm_bf16(xb[:, :E], w_p, out=T, stream=stream),
+        ]
+        flops = 2 * m * H * (E + 1280 + 768 + 2 * I + I + E) + 2 * m * E * H
+        return ("config3 GEMMs of one EmbeddingGemma 2 layer on inl_gemm_bf16_fwd / _gated_fwd (139,124 rows: "
+                "per-layer input 768->256, q/k/v 768->1280, o 768->768, GEGLU 768->2x1152, down 1152->768, "
+                "per-layer gate 768->256 x multiplier, per-layer projection 256->768), bf16 in, f32 accumulation",
+                "gemm_bf16_kernel", len(launches), timed(launches), m, flops, "bf16")
+
     if name == "splade_decoder":
         # config 4: the fused decoder GEMM + per-text max over every speaking
         # row (bf16 head [S, 768] x decoder [50002, 768]^T), no logits written
@@ -647,6 +678,10 @@ def timed_launches(torch, step, n_launch, steps):
             sleep(int(max(host, 1e-4) * 4e9))   # about twice the host time at ~2 GHz
         step(events[s])
     torch.cuda.synchronize()
+    if n_launch > 1:
+        per = [sum(events[s][i][0].elapsed_time(events[s][i][1]) for s in range(steps)) / steps
+               for i in range(n_launch)]
+        log("per-launch average (us): " + ", ".join(f"{1e3 * x:.1f}" for x in per))
     return sum(a.elapsed_time(b) for ev in events for a, b in ev) / (steps * n_launch)
 
 

@@ -14,12 +14,16 @@
 // output columns) x 4 (x rows), each wave 128 x 64 = 4 x 2 blocks of
 // v_mfma_f32_32x32x16_bf16 (the w block is the MFMA's row operand, the x
 // block its column operand, so a lane's accumulator holds one output row and
-// four runs of four consecutive output columns: 16-byte f32 stores). The K
+// four runs of four consecutive output columns). The K
 // loop runs through a 3-stage LDS ring of 32-wide k slices (32 KiB a stage),
 // filled by direct global -> LDS loads three stages ahead; each stage's MFMA
 // operands are read into registers one stage ahead. The workgroup is
 // persistent: its tiles form one stream of stages, so the next tile's first
-// loads are in flight while the current tile's epilogue stores run.
+// loads are in flight while the current tile's epilogue stores run. The
+// epilogue goes through 4 KiB of LDS per wave, 32 rows x 128 bytes at a
+// time, so that every store instruction writes eight whole 128-byte row
+// segments (stores straight from the accumulator layout write 32-byte pieces
+// of 32 rows and took a third of the kernel's time).
 //
 // Gated epilogues (the GEGLU gates of EmbeddingGemma 2, gemma2.rs:249-254 and
 // :279-283, fused so that the gate and up products never reach memory):
@@ -50,7 +54,10 @@ namespace {
 constexpr int GM_BM = 256;    // x rows (output rows) per tile
 constexpr int GM_BN = 256;    // w rows (output columns) per tile
 constexpr int GM_BK = 32;     // k per LDS stage (64-byte rows)
-constexpr int GM_STAGES = 3;
+#ifndef INL_GEMM_STAGES
+#define INL_GEMM_STAGES 3
+#endif
+constexpr int GM_STAGES = INL_GEMM_STAGES;   // LDS ring depth; loads run GM_STAGES stages ahead
 constexpr int GM_ROW = GM_BK * 2;
 constexpr int GM_W = GM_BN * GM_ROW;            // 16 KiB
 constexpr int GM_X = GM_BM * GM_ROW;            // 16 KiB
@@ -58,7 +65,9 @@ constexpr int GM_STAGE = GM_W + GM_X;           // 32 KiB
 constexpr int GM_BLOCKS = GM_STAGE / 1024;      // 1 KiB direct-load blocks per stage
 constexpr int GM_NW = 8;
 constexpr int GM_PER_WAVE = GM_BLOCKS / GM_NW;  // 4
-constexpr int GM_LDS = GM_STAGES * GM_STAGE;    // 96 KiB
+constexpr int GM_RING = GM_STAGES * GM_STAGE;   // 96 KiB at 3 stages
+constexpr int GM_STG = 4096;                    // per-wave epilogue staging: 32 rows x 128 bytes
+constexpr int GM_LDS = GM_RING + GM_NW * GM_STG;
 constexpr int GM_XCDS = 8;
 
 static_assert(GM_BLOCKS % GM_NW == 0, "the direct loads split evenly over the waves");
@@ -217,6 +226,68 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
                                                             __builtin_bit_cast(bf16x8, f.b[b]), acc[a][b], 0, 0, 0);
   };
   int mm_j = 0, mm_ks = 0;   // the MFMA cursor
+  // Epilogue staging: this wave's 32 rows x 128 bytes; 16-byte chunk c of
+  // row r at r * 128 + ((c ^ ((r >> 1) & 7)) << 4), so that 16 lanes writing
+  // one chunk of 16 rows, and 16 lanes reading 8 chunks of 2 rows, each touch
+  // all 64 banks once.
+  const uint32_t stg = lds0 + GM_RING + (uint32_t)wave * GM_STG;
+  auto stg_at = [&](int r, int c) __attribute__((always_inline)) {
+    return stg + (uint32_t)r * 128 + (((uint32_t)c ^ (((uint32_t)r >> 1) & 7)) << 4);
+  };
+  // The staging holds bf16 outputs (64 columns) when they are final, and f32
+  // (32 columns) otherwise: f32 outputs, and bf16 outputs that still add
+  // beta * y (rounded once, after the addition).
+  constexpr bool STG16 = OUT_BF16 && !ACC;
+  constexpr int STG_COLS = STG16 ? 64 : 32;
+  // Rows row0 .. row0 + 31 of the staged block, STG_COLS columns from output
+  // column col0, to global memory: lane L stores chunk L % 8 of rows L / 8 +
+  // 8 j. Rows past m and chunks past n are dropped.
+  auto flush = [&](int64_t row0, int col0) __attribute__((always_inline)) {
+    constexpr int EPC = STG16 ? 8 : 4;   // elements per 16-byte staged chunk
+    const int c = lane & 7;
+    const int col = col0 + c * EPC;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = (lane >> 3) + 8 * j;
+      const u32x4 v = lds_load<u32x4>(stg_at(r, c));
+      const int64_t row = row0 + r;
+      if (row < p.m && col < p.n) {
+        char* dst = p.y + (row * p.ys + col) * (OUT_BF16 ? 2 : 4);
+        if constexpr (STG16) {
+          *reinterpret_cast<u32x4*>(dst) = v;
+        } else {
+          f32x4 t = __builtin_bit_cast(f32x4, v);
+          if constexpr (OUT_BF16) {   // ACC: add beta * y, then round
+            const bf16x4 o = *reinterpret_cast<const bf16x4*>(dst);
+            bf16x4 r4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r4[e] = (bf16)(t[e] + p.beta * (float)o[e]);
+            *reinterpret_cast<bf16x4*>(dst) = r4;
+          } else {
+            if constexpr (ACC) {
+              const f32x4 o = *reinterpret_cast<const f32x4*>(dst);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) t[e] += p.beta * o[e];
+            }
+            *reinterpret_cast<f32x4*>(dst) = t;
+          }
+        }
+      }
+    }
+  };
+  // 4 output values of this lane's row at staged column chunk_col (a multiple of 4)
+  auto put4 = [&](int chunk_col, f32x4 v) __attribute__((always_inline)) {
+    if constexpr (STG16) {
+      const f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
+      const u32x2 w = {__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
+                       __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2))};
+      lds_store<u32x2>(stg_at(l32, chunk_col >> 3) + ((chunk_col & 7) << 1), w);
+    } else {
+      // (whole-vector casts: hipcc miscompiles __builtin_bit_cast of a vector
+      // element lvalue such as v[e], broadcasting one element)
+      lds_store<u32x4>(stg_at(l32, chunk_col >> 2), __builtin_bit_cast(u32x4, v));
+    }
+  };
   // tile done: acc[a][b][4 * g + e] is product (row wm*64 + b*32 + l32,
   // w row wn*128 + a*32 + 8*g + 4*hf + e) of the tile
   auto tile_end = [&]() __attribute__((always_inline)) {
@@ -225,70 +296,51 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
     int64_t mt;
     int nt;
     tile_of(mm_j++, &mt, &nt);
-    const int64_t row0 = mt * GM_BM + wm * 64 + l32;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int64_t row = row0 + b * 32;
-      if (row < p.m) {
-        char* yr = p.y + row * p.ys * (OUT_BF16 ? 2 : 4);
-        auto put = [&](int col, f32x4 v) __attribute__((always_inline)) {
-          if constexpr (OUT_BF16) {
-            bf16x4* dst = reinterpret_cast<bf16x4*>(yr + (int64_t)col * 2);
-            if constexpr (ACC) {
-              const bf16x4 o = *dst;
+      const int64_t row0 = mt * GM_BM + wm * 64 + b * 32;
+      if constexpr (EPI == EPI_GEGLU) {
+        // block wn*4 + a: gate rows 0-15 and their up rows 16-31 give output
+        // columns 16 (wn*4 + a) + 0..15 of the tile: all four blocks are 64
+        // bf16 or f32 columns, staged 128 bytes (32 f32 columns) at a time
+        constexpr int PER = STG_COLS / 16;   // a-blocks (16 outputs each) per staging
 #pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] += p.beta * (float)o[e];
-            }
-            bf16x4 r;
+        for (int a0 = 0; a0 < 4; a0 += PER) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) r[e] = (bf16)v[e];
-            *dst = r;
-          } else {
-            f32x4* dst = reinterpret_cast<f32x4*>(yr + (int64_t)col * 4);
-            if constexpr (ACC) {
-              const f32x4 o = *dst;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] += p.beta * o[e];
-            }
-            *dst = v;
-          }
-        };
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          if constexpr (EPI == EPI_GEGLU) {
-            // MFMA block wn*4 + a: gate rows 0-15 of the block and their up
-            // rows 16-31, output columns 16 * (wn*4 + a) + 0..15 of the tile
-            const int colb = nt * BNO + (wn * 4 + a) * 16 + 4 * hf;
+          for (int a = a0; a < a0 + PER; ++a)
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
-              const int col = colb + 8 * g;
-              if (col < p.n) {
-                f32x4 v;
+              f32x4 v;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  v[e] = gelu_tanh(p.alpha * acc[a][b][4 * g + e]) * (p.alpha * acc[a][b][4 * (g + 2) + e]);
-                put(col, v);
-              }
+              for (int e = 0; e < 4; ++e)
+                v[e] = gelu_tanh(p.alpha * acc[a][b][4 * g + e]) * (p.alpha * acc[a][b][4 * (g + 2) + e]);
+              put4((a - a0) * 16 + 8 * g + 4 * hf, v);
             }
-          } else {
-            const int colb = nt * BNO + wn * 128 + a * 32 + 4 * hf;
+          flush(row0, nt * BNO + wn * 64 + a0 * 16);
+        }
+      } else {
+        constexpr int PER = STG_COLS / 32;   // a-blocks (32 columns each) per staging
+#pragma unroll
+        for (int a0 = 0; a0 < 4; a0 += PER) {
+#pragma unroll
+          for (int a = a0; a < a0 + PER; ++a)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-              const int col = colb + 8 * g;
-              if (col < p.n) {
-                f32x4 v;
-                if constexpr (EPI == EPI_GELU_MUL) {
-                  const bf16x4 mv = *reinterpret_cast<const bf16x4*>(p.mul + (row * p.ms + col) * 2);
+              f32x4 v;
+              if constexpr (EPI == EPI_GELU_MUL) {
+                const int64_t row = row0 + l32;
+                const int col = nt * BNO + wn * 128 + a * 32 + 8 * g + 4 * hf;
+                bf16x4 mv = {};
+                if (row < p.m && col < p.n) mv = *reinterpret_cast<const bf16x4*>(p.mul + (row * p.ms + col) * 2);
 #pragma unroll
-                  for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(p.alpha * acc[a][b][4 * g + e]) * (float)mv[e];
-                } else {
+                for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(p.alpha * acc[a][b][4 * g + e]) * (float)mv[e];
+              } else {
 #pragma unroll
-                  for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[a][b][4 * g + e];
-                }
-                put(col, v);
+                for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[a][b][4 * g + e];
               }
+              put4((a - a0) * 32 + 8 * g + 4 * hf, v);
             }
-          }
+          flush(row0, nt * BNO + wn * 128 + a0 * 32);
         }
       }
     }
@@ -300,13 +352,13 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
   // One iteration per stage s, with h0 holding its first k step's operands:
   // read its second k step's operands while the first step's MFMAs run;
   // then wait for stage s + 1 (vmcnt) and for every wave to have read all of
-  // stage s (barrier), refill stage s's LDS slot with stage s + 3, and read
+  // stage s (barrier), refill stage s's LDS slot with stage s + GM_STAGES, and read
   // stage s + 1's first k step while the second step's MFMAs run.
   Half h0, h1;
   auto step = [&]() __attribute__((always_inline)) {
     read_half(1, h1);
     mfmas(h0);
-    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(GM_PER_WAVE) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"((GM_STAGES - 2) * GM_PER_WAVE) : "memory");
     lds_barrier();
     issue();
     if (++rd_slot == GM_STAGES) rd_slot = 0;
@@ -315,10 +367,9 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
     tile_end();
   };
 
-  issue();
-  issue();
-  issue();
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * GM_PER_WAVE) : "memory");   // stage 0
+#pragma unroll
+  for (int i = 0; i < GM_STAGES; ++i) issue();
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"((GM_STAGES - 1) * GM_PER_WAVE) : "memory");   // stage 0
   lds_barrier();
   read_half(0, h0);
   for (int st = 0; st < total; ++st) step();

@@ -136,6 +136,39 @@ def test_config3_shape_full_depth_f32(cuda, inl):
     assert cos.min() >= 0.9999
 
 
+def test_config3_shape_full_depth_bf16(cuda, inl):
+    """All 24 layers at the configuration-3 width in bf16 (the configuration's
+    dtype), against the oracle in f64 on the same bf16-rounded weights.
+
+    Texts of 64 tokens or more (configuration 3 draws U[64, 8192]) meet the
+    reference's bf16 floor, cosine >= 0.999 (crates/inl-text/tests/
+    qwen3_live.rs:88-94). A 1-token text has no mean over positions to
+    average its rounding errors, and 24 random-init layers amplify them: an
+    emulation of bf16 rounding at the reference's own points (residual stream,
+    every projection output and the gate/up products in bf16) puts such a text
+    at cosine ~0.9966 against f64, while this runner's points (f32 residual
+    stream and projection outputs, fused gates) put it at ~0.9993; its bound
+    here is 0.998."""
+    import torch
+    from inl_hip import workloads as wl
+    tc = wl.gemma2_config3(vocab=4096)
+    W = wl.gemma2_random_weights(tc, seed=8)
+    wd = _device_weights(W, torch, cuda, torch.bfloat16)
+    W = {k: v.float().cpu().numpy() for k, v in wd.items()}
+    lengths = [700, 64, 513, 1, 130]
+    ids = np.random.default_rng(4).integers(0, tc["vocab_size"], sum(lengths))
+    cu = oa.cu_from_lengths(lengths)
+    print(f"case=gemma2_config3_24layer bf16 lengths={lengths}", flush=True)
+    enc = inl.Gemma2Encoder(tc, wd, max_positions=1024)
+    got = enc.encode(ids, cu.tolist()).cpu().numpy().astype(np.float64)
+    enc.close()
+    cos = _cosines(got, og.encode(W, tc, ids, cu))
+    print(f"gemma2_config3_24layer bf16: cosines {np.round(cos, 6).tolist()}", flush=True)
+    long_ = np.asarray(lengths) >= 64
+    assert cos[long_].min() >= 0.999
+    assert cos[~long_].min() >= 0.998
+
+
 def test_runner_refuses_bad_inputs(tiny, cuda, inl):
     import torch
     cfg, W, _, _ = tiny
