@@ -140,6 +140,80 @@ __global__ __launch_bounds__(256) void post_add_kernel(int64_t rows, int32_t dim
   }
 }
 
+// post_add_kernel with 16-byte accesses: lane l handles the 4-element
+// groups l, l + 64, ... of the row (dim a multiple of 4, rows and weights
+// 16-byte / 8-byte aligned), NV groups at most.
+template <typename TW, typename TX, int NV>
+__global__ __launch_bounds__(256) void post_add_vec_kernel(int64_t rows, int32_t dim, float* h, const float* t,
+                                                           const char* w1, const char* scalar, float eps,
+                                                           const char* w2, char* x) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const int ng = dim >> 2;
+  f32x4* hr = reinterpret_cast<f32x4*>(h + r * dim);
+  const f32x4* tr = reinterpret_cast<const f32x4*>(t + r * dim);
+  auto w4 = [&](const char* w, int g) __attribute__((always_inline)) {
+    f32x4 o;
+    if constexpr (sizeof(TW) == 2) {
+      const bf16x4 b = reinterpret_cast<const bf16x4*>(w)[g];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (float)b[e];
+    } else {
+      o = reinterpret_cast<const f32x4*>(w)[g];
+    }
+    return o;
+  };
+  f32x4 tv[NV], hv[NV];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int g = lane + 64 * j;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    tv[j] = g < ng ? tr[g] : z;
+    hv[j] = g < ng ? hr[g] : z;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += tv[j][e] * tv[j][e];
+  }
+  const float inv1 = 1.0f / sqrtf(wave_sum(ss) / (float)dim + eps);
+  const float s = scalar ? ldv<TW>(scalar, 0) : 1.f;
+  float ss2 = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int g = lane + 64 * j;
+    if (g < ng) {
+      const f32x4 wv = w4(w1, g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hv[j][e] = (hv[j][e] + tv[j][e] * inv1 * wv[e]) * s;
+      hr[g] = hv[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss2 += hv[j][e] * hv[j][e];
+    }
+  }
+  char* xr = x + r * dim * (int64_t)sizeof(TX);
+  const float inv2 = w2 ? 1.0f / sqrtf(wave_sum(ss2) / (float)dim + eps) : 1.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int g = lane + 64 * j;
+    if (g < ng) {
+      f32x4 o = hv[j];
+      if (w2) {
+        const f32x4 wv = w4(w2, g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = o[e] * inv2 * wv[e];
+      }
+      if constexpr (sizeof(TX) == 2) {
+        bf16x4 b;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b[e] = (bf16)o[e];
+        reinterpret_cast<bf16x4*>(xr)[g] = b;
+      } else {
+        reinterpret_cast<f32x4*>(xr)[g] = o;
+      }
+    }
+  }
+}
+
 // y[r, i] = gelu_tanh(a[r, i]) * b[r, i], i < n, all in T, rows strided
 // (elements): the GEGLU gate of the MLP and of the per-layer-input block.
 // gelu_tanh(v) = v / 2 * (1 + tanh(sqrt(2 / pi) * (v + 0.044715 v^3))) in f32.
@@ -193,6 +267,14 @@ int launch_post_add(int dt, int64_t rows, int32_t dim, float* h, const float* t,
   const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   const char *a = (const char*)w1, *s = (const char*)scalar, *b = (const char*)w2;
   char* xo = (char*)x;
+  const uintptr_t wal = dt == INL_BF16 ? 7 : 15;
+  if (dim % 4 == 0 && dim <= 64 * 4 * 4 && ((uintptr_t)h & 15) == 0 && ((uintptr_t)t & 15) == 0 &&
+      ((uintptr_t)x & wal) == 0 && ((uintptr_t)w1 & wal) == 0 && ((uintptr_t)w2 & wal) == 0) {
+    if (dt == INL_BF16) hipLaunchKernelGGL((post_add_vec_kernel<bf16, bf16, 4>), grid, block, 0, st, rows, dim, h, t, a, s, eps, b, xo);
+    else hipLaunchKernelGGL((post_add_vec_kernel<float, float, 4>), grid, block, 0, st, rows, dim, h, t, a, s, eps, b, xo);
+    INL_HIP_TRY(hipGetLastError());
+    return INL_OK;
+  }
   if (dt == INL_BF16) {
     if (dim <= 64 * 16) hipLaunchKernelGGL((post_add_kernel<bf16, bf16, 16>), grid, block, 0, st, rows, dim, h, t, a, s, eps, b, xo);
     else hipLaunchKernelGGL((post_add_kernel<bf16, bf16, 64>), grid, block, 0, st, rows, dim, h, t, a, s, eps, b, xo);
@@ -569,17 +651,13 @@ extern "C" int inl_gemma2_encode(inl_gemma2* e, int32_t n_texts, const int32_t* 
     if (!rc) rc = inl_rms_norm_rows_fwd(n, c.ple_dim, T, E, e->ple_norm, dt, c.eps, dt, P, E, stream);
     if (i == 0 && !rc) rc = inl_rms_norm_rows_fwd(n, c.hidden, h, H, w.input_norm, dt, c.eps, dt, x, H, stream);
     if (!rc) rc = gemm(dt, n, qkv_w, H, x, H, w.qkv_proj, H, dt, A, L.a_w, 1.f, gws, gws_bytes, stream);
+    // q (q_norm, rope), k (k_norm, rope) and v (weightless, no rope) of the
+    // fused row in one launch
     nr.head_dim = s.hd;
     nr.rotary_dim = s.hd;
-    nr.heads = c.heads;
-    if (!rc) rc = inl_norm_rope_fwd(&nr, A, A, w.q_norm, d_pos, e->cos[s.full], e->sin[s.full], nullptr, nullptr,
-                                    stream);
-    nr.heads = s.kvh;
-    if (!rc) rc = inl_norm_rope_fwd(&nr, A + qd * es, A + qd * es, w.k_norm, d_pos, e->cos[s.full], e->sin[s.full],
-                                    nullptr, nullptr, stream);
-    nr.rotary_dim = 0;
-    if (!rc) rc = inl_norm_rope_fwd(&nr, A + (qd + kvd) * es, A + (qd + kvd) * es, nullptr, d_pos, nullptr, nullptr,
-                                    nullptr, nullptr, stream);
+    nr.heads = c.heads + 2 * s.kvh;
+    if (!rc) rc = norm_rope_launch_ex(&nr, A, A, w.q_norm, w.k_norm, c.heads, c.heads + s.kvh, c.heads + s.kvh, d_pos,
+                                      e->cos[s.full], e->sin[s.full], nullptr, nullptr, stream);
     if (!rc) rc = inl_attn_fwd(plans[pk], A, A + qd * es, A + (qd + kvd) * es, B, stream);
     if (!rc) rc = gemm(dt, n, H, qd, B, L.b_w, w.o_proj, qd, INL_F32, T, H, 1.f, gws, gws_bytes, stream);
     if (!rc) rc = launch_post_add(dt, n, c.hidden, h, T, w.post_attention_norm, nullptr, c.eps, w.pre_feedforward_norm,

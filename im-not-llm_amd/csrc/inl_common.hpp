@@ -45,11 +45,18 @@ int set_max_dynamic_lds(const void* fn, int bytes);
 // count through `total`.
 int check_cu(int32_t n, const int32_t* cu, int64_t* total);
 
-// inl_norm_rope_fwd with heads >= w2_heads (a multiple of 4) normalised with
+// inl_norm_rope_fwd with heads >= w2_heads normalised with
 // weight2: the q and k heads of one fused QKV row in one launch.
 int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const void* weight,
                      const void* weight2, int32_t w2_heads, const int32_t* rows, const float* cos,
                      const float* sin, const float* cos2, const float* sin2, void* stream);
+// The same with per-head ranges: heads [0, w2_heads) normalised with weight,
+// [w2_heads, w3_heads) with weight2, the rest with none; heads from
+// rope_heads on are not rotated (one launch for a fused q/k/v row).
+int norm_rope_launch_ex(const inl_norm_rope_desc* d, const void* x, void* y, const void* weight,
+                        const void* weight2, int32_t w2_heads, int32_t w3_heads, int32_t rope_heads,
+                        const int32_t* rows, const float* cos, const float* sin, const float* cos2,
+                        const float* sin2, void* stream);
 
 // Pinned host staging for a runner's per-call uploads (token ids, positions,
 // offsets, attention schedules). A call waits until the copies of the

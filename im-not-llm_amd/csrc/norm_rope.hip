@@ -14,6 +14,7 @@
 // 289-300, crates/inl-vision/src/vision.rs:792-800).
 
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 #include "inl_common.hpp"
@@ -29,6 +30,8 @@ struct NormRopeParams {
   const char* w;            // [head_dim] in x dtype, or null
   const char* w2;           // heads >= w2_heads use this weight instead (null: none)
   int32_t w2_heads;
+  int32_t w3_heads;         // heads >= w3_heads are normalised without a weight
+  int32_t rope_heads;       // heads >= rope_heads are not rotated
   const int32_t* rows;      // table row per token
   const float* cos;
   const float* sin;
@@ -129,15 +132,17 @@ __device__ __forceinline__ void xor_lanes8(const float (&in)[8], float (&out)[8]
   }
 }
 // A group of G = head_dim / 8 lanes owns one token: each lane holds 8
-// elements of a head row. The token's norm weight, table row and the lane's
-// cos/sin columns are loaded once per group of HB = 4 heads of the token
+// elements of a head row. The token's norm weights, table row and the lane's
+// cos/sin columns are loaded once per group of HB (4 or 8) heads of the token
 // (each lane group owns one (token, head chunk)), so per (token, head) x is
-// read and y written and the tables cost a quarter of that in cache reads;
-// the 4 loads of a lane go out together. Every lane of a wave runs the head
-// step the same number of times (the shuffles need all of them).
-template <typename TI, typename TO, int G>
+// read and y written and the tables cost 1/HB of that in cache reads; the
+// HB loads of a lane go out together. Heads [0, w2_heads) take weight w,
+// [w2_heads, w3_heads) weight w2 and the rest none; heads from rope_heads on
+// are normalised only (a fused q/k/v row: q and k rotated, v not). Every
+// lane of a wave runs the head step the same number of times (the shuffles
+// need all of them).
+template <typename TI, typename TO, int G, int HB>
 __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
-  constexpr int HB = 4;                          // heads per step
   // G = head_dim / 8 lanes per row (a power of two <= 64)
   const int lane = threadIdx.x & 63;
   const int j = lane & (G - 1);                  // chunk of the row this lane owns
@@ -163,11 +168,11 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
   for (int i = 0; i < HB; ++i) load8<TI>(xt + min(hfirst + i, heads - 1) * hstep_x, v[i]);
 
   // ---- per-token constants ----
-  float w[8];
+  float w[8], w2[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) w[e] = 1.f;
-  const char* wsel = p.w2 && hfirst >= p.w2_heads ? p.w2 : p.w;
-  if (p.norm && wsel) load8<TI>(wsel + 8 * j * (int)sizeof(TI), w);
+  for (int e = 0; e < 8; ++e) w[e] = w2[e] = 1.f;
+  if (p.norm && p.w && hfirst < p.w2_heads) load8<TI>(p.w + 8 * j * (int)sizeof(TI), w);
+  if (p.norm && p.w2 && hfirst + HB > p.w2_heads && hfirst < p.w3_heads) load8<TI>(p.w2 + 8 * j * (int)sizeof(TI), w2);
 
   // rope geometry: `mode` 0 = none for this lane, 1 = pairs (e, e + 4) inside
   // the lane (rotary_dim 8), 2 = half-split with the partner lane
@@ -247,13 +252,17 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
         for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
         ss = group_sum<G>(ss);
         const float inv = 1.0f / sqrtf(ss / (float)p.head_dim + p.eps);
+        const int h = h0 + i;
+        const int wk = h < p.w2_heads ? 0 : (h < p.w3_heads ? 1 : 2);   // uniform in the lane group
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          v[i][e] = v[i][e] * inv * w[e];
+          const float we = wk == 0 ? w[e] : (wk == 1 ? w2[e] : 1.f);
+          v[i][e] = v[i][e] * inv * we;
           if (p.round_norm && sizeof(TO) == 2) v[i][e] = round_bf16(v[i][e]);
         }
       }
-      if (mode == 1) {
+      const bool rot = h0 + i < p.rope_heads;
+      if (mode == 1 && rot) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float a = v[i][e], b = v[i][e + 4];
@@ -268,12 +277,12 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
         else
 #pragma unroll
           for (int e = 0; e < 8; ++e) pv[e] = __shfl(v[i][e], partner, 64);
-        if (mode == 2)
+        if (mode == 2 && rot)
 #pragma unroll
           for (int e = 0; e < 8; ++e)
             v[i][e] = first ? (v[i][e] * c[e] - pv[e] * sn[e]) : (v[i][e] * c[e] + pv[e] * sn[e]);
       }
-      if (bad_pos)
+      if (bad_pos && rot)
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[i][e] = __builtin_nanf("");
       if (valid && h0 + i < heads) store8<TO>(yt + (h0 + i) * hstep_y, v[i]);
@@ -287,11 +296,13 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
 
 namespace inl {
 
-// inl_norm_rope_fwd, with heads >= w2_heads (a multiple of the kernel's
-// 4-head step) normalised with weight2 instead of weight.
-int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const void* weight,
-                     const void* weight2, int32_t w2_heads, const int32_t* rows, const float* cos,
-                     const float* sin, const float* cos2, const float* sin2, void* stream) {
+// inl_norm_rope_fwd with per-head ranges: heads [0, w2_heads) normalised
+// with weight, [w2_heads, w3_heads) with weight2, the rest without a weight;
+// heads from rope_heads on are not rotated.
+int norm_rope_launch_ex(const inl_norm_rope_desc* d, const void* x, void* y, const void* weight,
+                        const void* weight2, int32_t w2_heads, int32_t w3_heads, int32_t rope_heads,
+                        const int32_t* rows, const float* cos, const float* sin, const float* cos2,
+                        const float* sin2, void* stream) {
   if (!d) return fail(INL_E_INVALID, "norm_rope: desc is NULL");
   if (!dtype_ok(d->dtype) || !dtype_ok(d->out_dtype))
     return fail(INL_E_INVALID, "norm_rope: dtype must be INL_F32 or INL_BF16");
@@ -325,15 +336,18 @@ int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const 
   if (!x || !y || ((uintptr_t)x & 15) || ((uintptr_t)y & 15) || (weight && ((uintptr_t)weight & 15)) ||
       (weight2 && ((uintptr_t)weight2 & 15)))
     return fail(INL_E_INVALID, "norm_rope: x, y and weight must be non-null and 16-byte aligned");
-  if (weight2 && (w2_heads <= 0 || w2_heads % 4 || w2_heads >= d->heads))
-    return fail(INL_E_INVALID, "norm_rope: the second weight's first head must be a multiple of 4 inside the heads");
+  if (w2_heads < 0 || w2_heads > w3_heads || w3_heads > d->heads || rope_heads < 0 || rope_heads > d->heads ||
+      (weight2 && w2_heads == w3_heads))
+    return fail(INL_E_INVALID, "norm_rope: head ranges must satisfy 0 <= w2_heads <= w3_heads <= heads");
 
   NormRopeParams p{};
   p.x = (const char*)x;
   p.y = (char*)y;
   p.w = d->norm ? (const char*)weight : nullptr;
   p.w2 = d->norm ? (const char*)weight2 : nullptr;
-  p.w2_heads = weight2 ? w2_heads : 0;
+  p.w2_heads = w2_heads;
+  p.w3_heads = w3_heads;
+  p.rope_heads = rope_heads;
   p.rows = rows;
   p.cos = cos;
   p.sin = sin;
@@ -353,8 +367,11 @@ int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const 
   p.round_norm = d->round_norm;
 
   const int G = hd >> 3;
+  // heads per lane group: 8 for 5-7 heads (a fused q/k/v row: one group per
+  // token), else 4 (8 was slower on 8 and 16 heads of head_dim 128)
+  const int HB = d->heads > 4 && d->heads < 8 ? 8 : 4;
   const int64_t groups_per_block = 256 / G;
-  const int64_t groups = d->n_tokens * ((d->heads + 3) / 4);   // (token, 4-head chunk)
+  const int64_t groups = d->n_tokens * ((d->heads + HB - 1) / HB);   // (token, HB-head chunk)
   if (groups + groups_per_block >= ((int64_t)1 << 31))
     return fail(INL_E_UNSUPPORTED, "norm_rope: tokens x head chunks must stay below 2^31");
   const int64_t blocks = (groups + groups_per_block - 1) / groups_per_block;
@@ -363,15 +380,20 @@ int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const 
     using TI = decltype(ti);
     using TO = decltype(to);
     const dim3 grid((unsigned)blocks), block(256);
-    switch (G) {
-      case 1: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 1>), grid, block, 0, st, p); break;
-      case 2: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 2>), grid, block, 0, st, p); break;
-      case 4: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 4>), grid, block, 0, st, p); break;
-      case 8: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 8>), grid, block, 0, st, p); break;
-      case 16: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 16>), grid, block, 0, st, p); break;
-      case 32: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 32>), grid, block, 0, st, p); break;
-      default: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 64>), grid, block, 0, st, p);
-    }
+    auto go = [&](auto hb) {
+      constexpr int H = decltype(hb)::value;
+      switch (G) {
+        case 1: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 1, H>), grid, block, 0, st, p); break;
+        case 2: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 2, H>), grid, block, 0, st, p); break;
+        case 4: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 4, H>), grid, block, 0, st, p); break;
+        case 8: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 8, H>), grid, block, 0, st, p); break;
+        case 16: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 16, H>), grid, block, 0, st, p); break;
+        case 32: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 32, H>), grid, block, 0, st, p); break;
+        default: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 64, H>), grid, block, 0, st, p);
+      }
+    };
+    if (HB == 8) go(std::integral_constant<int, 8>{});
+    else go(std::integral_constant<int, 4>{});
   };
   if (d->dtype == INL_BF16 && d->out_dtype == INL_BF16) launch(bf16{}, bf16{});
   else if (d->dtype == INL_BF16) launch(bf16{}, float{});
@@ -379,6 +401,16 @@ int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const 
   else launch(float{}, float{});
   INL_HIP_TRY(hipGetLastError());
   return INL_OK;
+}
+
+int norm_rope_launch(const inl_norm_rope_desc* d, const void* x, void* y, const void* weight,
+                     const void* weight2, int32_t w2_heads, const int32_t* rows, const float* cos,
+                     const float* sin, const float* cos2, const float* sin2, void* stream) {
+  if (!d) return fail(INL_E_INVALID, "norm_rope: desc is NULL");
+  if (weight2 && (w2_heads <= 0 || w2_heads >= d->heads))
+    return fail(INL_E_INVALID, "norm_rope: the second weight's first head must lie inside the heads");
+  return norm_rope_launch_ex(d, x, y, weight, weight2, weight2 ? w2_heads : d->heads, d->heads, d->heads, rows, cos,
+                             sin, cos2, sin2, stream);
 }
 
 }  // namespace inl
