@@ -39,8 +39,11 @@ qwen3_e2e_bf16) time a whole Qwen3-0.6B encode of 8 texts (778 tokens) and
 report encoded tokens/s, with the numpy f32 forward as the CPU baseline;
 --workload gemma_e2e does the same for configuration 3 (the
 EmbeddingGemma-2 text tower, bf16, 32 texts of U[64,8192] tokens, every GEMM
-on the library's own bf16 kernel), with three of its texts checked against
-the oracle.
+on the library's own bf16 kernel); its CPU leg also checks three of the
+timed batch's texts against the oracle. The default line nests the
+configuration-1 end-to-end measurement (f32, a new 8-text draw every step)
+under `e2e_config1`; --workload gemm times one configuration-3 layer's GEMMs
+on the library's bf16 kernel.
 """
 from __future__ import annotations
 
@@ -454,15 +457,17 @@ def gemma_e2e_main(args):
                      "kernel": "whole encode (own bf16 MFMA GEMMs, attention, prologue, norms, GEGLU, pooling)",
                      "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": {"flop": flops}},
     }
-    result["parity"] = gemma_e2e_parity(host_w, tc, ids, cu, out, weights)
     if not args.no_cpu:
+        # the CPU leg: the oracle's forward as the baseline, and as the
+        # checker of three texts of the timed batch
         result["cpu_baseline"] = gemma_e2e_cpu_baseline(host_w, tc, args.cpu_seconds)
+        result["cpu_baseline"]["oracle_check"] = gemma_e2e_parity(host_w, tc, ids, cu, out, weights)
     enc.close()
     print(json.dumps(result), flush=True)
 
 
 def gemma_e2e_parity(host_w, tc, ids, cu, out, weights):
-    """Cosines of three texts of the timed batch (the shortest and the two
+    """(Part of the CPU leg.) Cosines of three texts of the timed batch (the shortest and the two
     nearest 1,000 tokens) against oracle/gemma2.py in f32 on the bf16-rounded
     weights: texts are independent in a packed batch, so the oracle encodes
     just those texts. The reference's bf16 floor is cosine >= 0.999."""
