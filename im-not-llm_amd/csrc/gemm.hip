@@ -43,6 +43,7 @@
 // HBM once, then from that XCD's 4 MB L2), and w (at most a few MB) stays in
 // L2 across the range.
 #include <algorithm>
+#include <type_traits>
 
 #include "../../include/inl_encoder.h"
 #include "attn_stream.hpp"
@@ -51,27 +52,40 @@ namespace inl {
 
 namespace {
 
-constexpr int GM_BM = 256;    // x rows (output rows) per tile
-constexpr int GM_BN = 256;    // w rows (output columns) per tile
+constexpr int GM_BN = 256;    // w rows (output columns) per tile: 2 waves x 128
 constexpr int GM_BK = 32;     // k per LDS stage (64-byte rows)
-#ifndef INL_GEMM_STAGES
-#define INL_GEMM_STAGES 3
-#endif
-constexpr int GM_STAGES = INL_GEMM_STAGES;   // LDS ring depth; loads run GM_STAGES stages ahead
 constexpr int GM_ROW = GM_BK * 2;
-constexpr int GM_W = GM_BN * GM_ROW;            // 16 KiB
-constexpr int GM_X = GM_BM * GM_ROW;            // 16 KiB
-constexpr int GM_STAGE = GM_W + GM_X;           // 32 KiB
-constexpr int GM_BLOCKS = GM_STAGE / 1024;      // 1 KiB direct-load blocks per stage
-constexpr int GM_NW = 8;
-constexpr int GM_PER_WAVE = GM_BLOCKS / GM_NW;  // 4
-constexpr int GM_RING = GM_STAGES * GM_STAGE;   // 96 KiB at 3 stages
+constexpr int GM_W = GM_BN * GM_ROW;            // 16 KiB of w rows per stage
 constexpr int GM_STG = 4096;                    // per-wave epilogue staging: 32 rows x 128 bytes
-constexpr int GM_LDS = GM_RING + GM_NW * GM_STG;
 constexpr int GM_XCDS = 8;
 
-static_assert(GM_BLOCKS % GM_NW == 0, "the direct loads split evenly over the waves");
-static_assert(GM_PER_WAVE % 2 == 0, "each wave loads w blocks then x blocks");
+// Kernel shape: NW waves as 2 (w rows) x NW / 2 (x rows), each 128 x 64;
+// an LDS ring of STAGES k slices; WPC workgroups per CU.
+template <int NW_, int STAGES_, int WPC_>
+struct GemmShape {
+  static constexpr int NW = NW_;
+  static constexpr int WMW = NW / 2;                // waves along x
+  static constexpr int BM = WMW * 64;               // x rows (output rows) per tile
+  static constexpr int STAGES = STAGES_;
+  static constexpr int WPC = WPC_;
+  static constexpr int X = BM * GM_ROW;
+  static constexpr int STAGE = GM_W + X;
+  static constexpr int BLOCKS = STAGE / 1024;       // 1 KiB direct-load blocks per stage
+  static constexpr int PER_WAVE = BLOCKS / NW;
+  static constexpr int W_PER_WAVE = GM_W / 1024 / NW;
+  static constexpr int RING = STAGES * STAGE;
+  static constexpr int LDS = RING + NW * GM_STG;
+  static_assert(BLOCKS % NW == 0 && (GM_W / 1024) % NW == 0, "the direct loads split evenly over the waves");
+  static_assert(NW % 2 == 0, "w blocks of one wave share its parity (GEGLU)");
+  static_assert(STAGES >= 2 && (STAGES - 1) * PER_WAVE <= 63, "vmcnt range");
+};
+// 8 waves, 256 x 256 tiles, 3 stages, one workgroup per CU (128 KiB LDS);
+// 4 waves, 128 x 256 tiles, 2 stages, two workgroups per CU (64 KiB each), so
+// that one workgroup computes while the other drains its tile's stores.
+#ifndef INL_GEMM_SHAPE
+#define INL_GEMM_SHAPE 0
+#endif
+using GemmCfg = std::conditional_t<INL_GEMM_SHAPE == 1, GemmShape<4, 2, 2>, GemmShape<8, 3, 1>>;
 
 enum GemmEpi { EPI_PLAIN = 0, EPI_GEGLU = 1, EPI_GELU_MUL = 2 };
 
@@ -100,7 +114,10 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 }
 
 template <int EPI, bool OUT_BF16, bool ACC>
-__global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
+__global__ __launch_bounds__(GemmCfg::NW * 64, GemmCfg::WPC) void gemm_bf16_kernel(GemmParams p) {
+  using C = GemmCfg;
+  constexpr int GM_NW = C::NW, GM_BM = C::BM, GM_STAGES = C::STAGES, GM_STAGE = C::STAGE;
+  constexpr int GM_PER_WAVE = C::PER_WAVE, GM_RING = C::RING;
   // output columns per tile: a GEGLU tile's 256 w rows are 128 gate + 128 up
   constexpr int BNO = EPI == EPI_GEGLU ? GM_BN / 2 : GM_BN;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
@@ -118,18 +135,18 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wave >> 2, wm = wave & 3;
+  const int wn = wave / C::WMW, wm = wave % C::WMW;
   const int l32 = lane & 31, hf = lane >> 5;
 
   // per-lane offsets of this wave's direct-load blocks inside a tile: blocks
-  // {wave, wave + 8, ...} of the 32 per stage, w rows (blocks 0-15) then x rows
+  // {wave, wave + NW, ...} of the stage, w rows (blocks 0-15) then x rows
   uint32_t goff[GM_PER_WAVE];
 #pragma unroll
   for (int i = 0; i < GM_PER_WAVE; ++i) {
     const int blk = wave + GM_NW * i;
     const int r = lane >> 2, cp = lane & 3;
     const int c = cp ^ ((r >> 2) & 3);
-    const bool is_w = i < GM_PER_WAVE / 2;
+    const bool is_w = i < C::W_PER_WAVE;
     // GEGLU: w block blk is 16-row chunk blk / 2 of the gate rows (blk even)
     // or of the up rows (blk odd); every w block of a wave has the wave's parity
     const int row = (is_w ? (EPI == EPI_GEGLU ? blk >> 1 : blk) : blk - GM_W / 1024) * 16 + r;
@@ -175,7 +192,7 @@ __global__ __launch_bounds__(GM_NW * 64) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < GM_PER_WAVE; ++i) {
       const int blk = wave + GM_NW * i;
-      const bool is_w = i < GM_PER_WAVE / 2;
+      const bool is_w = i < C::W_PER_WAVE;
       dma_b128(live ? (is_w ? wrs : xrs) : none, st + blk * 1024, goff[i] + koff);
     }
     if (++ld_slot == GM_STAGES) ld_slot = 0;
@@ -401,7 +418,7 @@ int gemm_launch(int epi, int64_t m, int64_t n, int64_t k, const void* x, int64_t
   if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)y & 15) || ((uintptr_t)mul & 7))
     return fail(INL_E_INVALID, "gemm: x, w and y must be 16-byte aligned, the multiplier 8-byte aligned");
   // each tile's descriptor spans at most 256 rows of x or w
-  if ((int64_t)GM_BM * xs * 2 >= ((int64_t)1 << 32) || (int64_t)GM_BN * ws * 2 >= ((int64_t)1 << 32))
+  if ((int64_t)GemmCfg::BM * xs * 2 >= ((int64_t)1 << 32) || (int64_t)GM_BN * ws * 2 >= ((int64_t)1 << 32))
     return fail(INL_E_UNSUPPORTED, "gemm: row strides too large for a tile's 32-bit buffer range");
   int dev = 0, cus = 0;
   INL_HIP_TRY(hipGetDevice(&dev));
@@ -422,10 +439,10 @@ int gemm_launch(int epi, int64_t m, int64_t n, int64_t k, const void* x, int64_t
   p.alpha = alpha;
   p.beta = beta;
   p.n_tiles_n = (int32_t)((n + bno - 1) / bno);
-  p.n_tiles = ((m + GM_BM - 1) / GM_BM) * p.n_tiles_n;
+  p.n_tiles = ((m + GemmCfg::BM - 1) / GemmCfg::BM) * p.n_tiles_n;
   p.per_xcd = (p.n_tiles + GM_XCDS - 1) / GM_XCDS;
-  // one workgroup per CU (96 KiB of LDS each), at most one per tile of an XCD's range
-  const int64_t per_xcd_wg = std::max<int64_t>(1, std::min<int64_t>(cus / GM_XCDS, p.per_xcd));
+  // GemmCfg::WPC workgroups per CU, at most one per tile of an XCD's range
+  const int64_t per_xcd_wg = std::max<int64_t>(1, std::min<int64_t>(cus / GM_XCDS * GemmCfg::WPC, p.per_xcd));
   p.wg_per_xcd = (int32_t)per_xcd_wg;
   if ((int64_t)(p.per_xcd + per_xcd_wg - 1) / per_xcd_wg * (k / GM_BK) >= ((int64_t)1 << 31))
     return fail(INL_E_UNSUPPORTED, "gemm: too many k stages per workgroup");
@@ -446,10 +463,10 @@ int gemm_launch(int epi, int64_t m, int64_t n, int64_t k, const void* x, int64_t
     default:
       return fail(INL_E_UNSUPPORTED, "gemm: the gated epilogues take beta = 0");
   }
-  int rc = set_max_dynamic_lds(fn, GM_LDS);
+  int rc = set_max_dynamic_lds(fn, GemmCfg::LDS);
   if (rc) return rc;
   void* args[] = {&p};
-  INL_HIP_TRY(hipLaunchKernel(fn, dim3((unsigned)(per_xcd_wg * GM_XCDS)), dim3(GM_NW * 64), args, GM_LDS,
+  INL_HIP_TRY(hipLaunchKernel(fn, dim3((unsigned)(per_xcd_wg * GM_XCDS)), dim3(GemmCfg::NW * 64), args, GemmCfg::LDS,
                               (hipStream_t)stream));
   return INL_OK;
 }

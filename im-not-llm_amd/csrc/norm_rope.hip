@@ -69,6 +69,33 @@ __device__ __forceinline__ void load8(const char* p, float (&v)[8]) {
   }
 }
 
+// A lane's 8 input values kept as loaded (bf16: one 16-byte vector, f32:
+// two) until the head step that uses them, so that the HB heads in flight
+// cost half the registers in bf16.
+struct Raw8 {
+  u32x4 a, b;
+};
+template <typename TI>
+__device__ __forceinline__ void load_raw(const char* p, Raw8& r) {
+  r.a = *reinterpret_cast<const u32x4*>(p);
+  if constexpr (sizeof(TI) != 2) r.b = *reinterpret_cast<const u32x4*>(p + 16);
+}
+template <typename TI>
+__device__ __forceinline__ void unpack8(const Raw8& r, float (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t a = r.a[j];
+    if constexpr (sizeof(TI) == 2) {
+      v[2 * j] = __builtin_bit_cast(float, a << 16);
+      v[2 * j + 1] = __builtin_bit_cast(float, a & 0xffff0000u);
+    } else {
+      const uint32_t b = r.b[j];
+      v[j] = __builtin_bit_cast(float, a);
+      v[4 + j] = __builtin_bit_cast(float, b);
+    }
+  }
+}
+
 template <typename TO>
 __device__ __forceinline__ void store8(char* p, const float (&v)[8]) {
   if constexpr (sizeof(TO) == 2) {
@@ -163,16 +190,19 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
   char* yt = p.y + ((int64_t)tok * p.y_stride + 8 * j) * (int64_t)sizeof(TO);
   const int64_t hstep_x = (int64_t)p.head_dim * (int64_t)sizeof(TI);
   const int64_t hstep_y = (int64_t)p.head_dim * (int64_t)sizeof(TO);
-  float v[HB][8];
+  Raw8 raw[HB];
 #pragma unroll
-  for (int i = 0; i < HB; ++i) load8<TI>(xt + min(hfirst + i, heads - 1) * hstep_x, v[i]);
+  for (int i = 0; i < HB; ++i) load_raw<TI>(xt + min(hfirst + i, heads - 1) * hstep_x, raw[i]);
 
   // ---- per-token constants ----
-  float w[8], w2[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) w[e] = w2[e] = 1.f;
-  if (p.norm && p.w && hfirst < p.w2_heads) load8<TI>(p.w + 8 * j * (int)sizeof(TI), w);
-  if (p.norm && p.w2 && hfirst + HB > p.w2_heads && hfirst < p.w3_heads) load8<TI>(p.w2 + 8 * j * (int)sizeof(TI), w2);
+  // the weights stay packed as loaded (ones when absent) until used
+  Raw8 wr, w2r;
+  {
+    const uint32_t one = sizeof(TI) == 2 ? 0x3f803f80u : 0x3f800000u;
+    wr.a = wr.b = w2r.a = w2r.b = (u32x4){one, one, one, one};
+  }
+  if (p.norm && p.w && hfirst < p.w2_heads) load_raw<TI>(p.w + 8 * j * (int)sizeof(TI), wr);
+  if (p.norm && p.w2 && hfirst + HB > p.w2_heads && hfirst < p.w3_heads) load_raw<TI>(p.w2 + 8 * j * (int)sizeof(TI), w2r);
 
   // rope geometry: `mode` 0 = none for this lane, 1 = pairs (e, e + 4) inside
   // the lane (rotary_dim 8), 2 = half-split with the partner lane
@@ -237,55 +267,57 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeParams p) {
     }
   }
 
-#pragma unroll
-  for (int i = 0; i < HB; ++i)
-    if (!(valid && hfirst + i < heads))
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
   {
     const int h0 = hfirst;   // this lane group's one step of HB heads
 #pragma unroll
     for (int i = 0; i < HB; ++i) {
+      float v[1][8];
+      unpack8<TI>(raw[i], v[0]);
+      if (!(valid && hfirst + i < heads))
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[0][e] = 0.f;
       if (p.norm) {
         float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+        for (int e = 0; e < 8; ++e) ss += v[0][e] * v[0][e];
         ss = group_sum<G>(ss);
         const float inv = 1.0f / sqrtf(ss / (float)p.head_dim + p.eps);
         const int h = h0 + i;
         const int wk = h < p.w2_heads ? 0 : (h < p.w3_heads ? 1 : 2);   // uniform in the lane group
+        float wv[8];
+        unpack8<TI>(wk == 0 ? wr : w2r, wv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float we = wk == 0 ? w[e] : (wk == 1 ? w2[e] : 1.f);
-          v[i][e] = v[i][e] * inv * we;
-          if (p.round_norm && sizeof(TO) == 2) v[i][e] = round_bf16(v[i][e]);
+          const float we = wk == 2 ? 1.f : wv[e];
+          v[0][e] = v[0][e] * inv * we;
+          if (p.round_norm && sizeof(TO) == 2) v[0][e] = round_bf16(v[0][e]);
         }
       }
       const bool rot = h0 + i < p.rope_heads;
       if (mode == 1 && rot) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float a = v[i][e], b = v[i][e + 4];
-          v[i][e] = a * c[e] - b * sn[e];
-          v[i][e + 4] = b * c[e] + a * sn[e];
+          const float a = v[0][e], b = v[0][e + 4];
+          v[0][e] = a * c[e] - b * sn[e];
+          v[0][e + 4] = b * c[e] + a * sn[e];
         }
       }
       if (p.rotary_dim > 0 && !(p.rotary_dim == 8 && p.sections == 1)) {
         float pv[8];
         if (xor_partner)
-          xor_lanes8(v[i], pv, half_lanes, lane);
+          xor_lanes8(v[0], pv, half_lanes, lane);
         else
 #pragma unroll
-          for (int e = 0; e < 8; ++e) pv[e] = __shfl(v[i][e], partner, 64);
+          for (int e = 0; e < 8; ++e) pv[e] = __shfl(v[0][e], partner, 64);
         if (mode == 2 && rot)
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            v[i][e] = first ? (v[i][e] * c[e] - pv[e] * sn[e]) : (v[i][e] * c[e] + pv[e] * sn[e]);
+            v[0][e] = first ? (v[0][e] * c[e] - pv[e] * sn[e]) : (v[0][e] * c[e] + pv[e] * sn[e]);
       }
       if (bad_pos && rot)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[i][e] = __builtin_nanf("");
-      if (valid && h0 + i < heads) store8<TO>(yt + (h0 + i) * hstep_y, v[i]);
+        for (int e = 0; e < 8; ++e) v[0][e] = __builtin_nanf("");
+      if (valid && h0 + i < heads) store8<TO>(yt + (h0 + i) * hstep_y, v[0]);
     }
   }
 }
