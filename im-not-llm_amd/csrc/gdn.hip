@@ -33,7 +33,15 @@ namespace {
 template <typename T>
 __device__ __forceinline__ float ld1(const T* p) { return (float)*p; }
 
-// Round an f32 to T and back (identity for f32).
+// One f32 value rounded to bf16 and back with one v_cvt_pk_bf16_f32: with
+// the value in the high half and +0 in the low half, the packed result is
+// already the f32 bit pattern of the rounded value.
+__device__ __forceinline__ float rnd1_bf16(float a) {
+  return __builtin_bit_cast(float, __builtin_convertvector((f32x2){0.f, a}, bf16x2));
+}
+
+// Round an f32 to T and back (identity for f32). (rnd1_bf16 in its place
+// measured 8 % slower in the gated norm, whose loads it rescheduled.)
 template <typename T>
 __device__ __forceinline__ float rnd(float x) { return (float)(T)x; }
 
@@ -67,12 +75,12 @@ __device__ __forceinline__ float silu_t(float x) {
   return rnd<T>(div_t<T>(x, d));
 }
 // silu_t<bf16> of two values that are bf16 already (so -x needs no rounding),
-// each rounding of the pair one conversion.
-__device__ __forceinline__ void silu2_bf16(float x0, float x1, float& y0, float& y1) {
-  float e0, e1, d0, d1;
-  rnd2_bf16(exp_t<bf16>(-x0), exp_t<bf16>(-x1), e0, e1);
-  rnd2_bf16(1.0f + e0, 1.0f + e1, d0, d1);
-  rnd2_bf16(div_t<bf16>(x0, d0), div_t<bf16>(x1, d1), y0, y1);
+// returned as the packed bf16 pair (the last rounding is the output's).
+__device__ __forceinline__ uint32_t silu2_bf16(float x0, float x1) {
+  const float e0 = rnd1_bf16(exp_t<bf16>(-x0)), e1 = rnd1_bf16(exp_t<bf16>(-x1));
+  const float d0 = rnd1_bf16(1.0f + e0), d1 = rnd1_bf16(1.0f + e1);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){div_t<bf16>(x0, d0), div_t<bf16>(x1, d1)},
+                                                             bf16x2));
 }
 
 // Index of the text holding packed row t: the last b with cu[b] <= t
@@ -177,20 +185,23 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const T* __restrict__ x, 
       for (int e = 0; e < V; ++e) cur[e] = ld1(x + t * xs + c0 + e);
     }
     float res[V];
+    uint32_t packed[V / 2 > 0 ? V / 2 : 1];   // bf16 pairs of the output row (bf16, V even)
     if constexpr (sizeof(T) == 2 && V % 2 == 0) {
 #pragma unroll
       for (int e = 0; e < V; e += 2) {
-        // tap k reads row t + k - (TAPS - 1): win[TAPS - 2 - k], the last tap cur
-        float a0 = 0.f, a1 = 0.f;
+        // tap k reads row t + k - (TAPS - 1): win[TAPS - 2 - k], the last tap
+        // cur. Each product and sum is rounded on its own (one conversion per
+        // value); the first sum, 0 + product, is exact (and turns -0 into +0).
+        float a[2];
 #pragma unroll
-        for (int k = 0; k < TAPS; ++k) {
-          const float s0 = k == TAPS - 1 ? cur[e] : win[TAPS - 2 - k][e];
-          const float s1 = k == TAPS - 1 ? cur[e + 1] : win[TAPS - 2 - k][e + 1];
-          float p0, p1;
-          rnd2_bf16(s0 * wt[k][e], s1 * wt[k][e + 1], p0, p1);
-          rnd2_bf16(a0 + p0, a1 + p1, a0, a1);
-        }
-        silu2_bf16(a0, a1, res[e], res[e + 1]);
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int k = 0; k < TAPS; ++k) {
+            const float sv = k == TAPS - 1 ? cur[e + h] : win[TAPS - 2 - k][e + h];
+            const float pr = rnd1_bf16(sv * wt[k][e + h]);
+            a[h] = k == 0 ? 0.f + pr : rnd1_bf16(a[h] + pr);
+          }
+        packed[e / 2] = silu2_bf16(a[0], a[1]);
       }
     } else {
 #pragma unroll
@@ -213,16 +224,15 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const T* __restrict__ x, 
 #pragma unroll
     for (int e = 0; e < V; ++e) win[0][e] = cur[e];
     if constexpr (VB) {
-      u32x4 o;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        o[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){res[2 * q], res[2 * q + 1]}, bf16x2));
-      *reinterpret_cast<u32x4*>(out + t * os + c0) = o;
+      *reinterpret_cast<u32x4*>(out + t * os + c0) = (u32x4){packed[0], packed[1], packed[2], packed[3]};
     } else if constexpr (VF) {
       f32x4 v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = res[e];
       *reinterpret_cast<f32x4*>(out + t * os + c0) = v;
+    } else if constexpr (sizeof(T) == 2 && V % 2 == 0) {
+#pragma unroll
+      for (int e = 0; e < V; e += 2) *reinterpret_cast<uint32_t*>(out + t * os + c0 + e) = packed[e / 2];
     } else {
 #pragma unroll
       for (int e = 0; e < V; ++e) out[t * os + c0 + e] = (T)res[e];
