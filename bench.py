@@ -28,7 +28,7 @@ Other attention workloads (--workload): gemma_window, gemma_full,
 modernbert_local, modernbert_global, vision, pplx_causal, qwen3_2048,
 qwen3_2048_full - reported the same way, and each of them in f32 with an
 `_f32` suffix (e.g. `qwen3_f32`: the f32 kernel against the 157.3 TFLOP/s
-fp32 matrix peak). Op workloads (--workload norm_rope,
+fp32 matrix peak). Op workloads (--workload norm_rope, norm_rope_qk,
 pool_last, pool_mean, splade, gdn_conv, gdn_gated_norm) time the prologue,
 epilogue and gated-delta-net element-wise kernels at their configurations'
 full sizes against the 8 TB/s HBM roofline; splade_decoder (a GEMM) against
@@ -200,8 +200,8 @@ def roofline(tflops, gbs, traffic, kernel, avg_ms, flop_launch, bytes_launch, pe
                       "frac": round(gbs / PEAK_HBM_GBS, 4)}}
 
 
-OP_WORKLOADS = ("norm_rope", "pool_last", "pool_mean", "splade", "splade_decoder", "gemm", "gdn_conv", "gdn_rule",
-                "gdn_gated_norm")
+OP_WORKLOADS = ("norm_rope", "norm_rope_qk", "pool_last", "pool_mean", "splade", "splade_decoder", "gemm",
+                "gdn_conv", "gdn_rule", "gdn_gated_norm")
 # What bounds each op workload that is not HBM-bound: the decoder is a GEMM
 # on the bf16 matrix cores; the delta rule is f32 vector (VALU) work, graded
 # against MI355X's 157.3 TFLOP/s fp32 vector peak (which counts packed-fp32
@@ -538,6 +538,31 @@ def op_workload(name, torch, inl_hip, dev):
                 nbytes += T * heads * 128 * 2 * 2 + T * 4 + 128 * 2 + max(b) * 64 * 4 * 2
         label = (f"config2 prologue: q/k RMSNorm+RoPE (Qwen3-0.6B: 16 q / 8 k heads x 128, bf16 in/out, "
                  f"theta 1e6) over {sum(lens)} tokens in 12 batches, 2 launches per batch")
+        return label, "norm_rope_kernel<bf16, bf16>", len(launches), timed(launches), sum(lens), nbytes, "bf16"
+    if name == "norm_rope_qk":
+        # the same prologue with q and k of each batch in one launch
+        # (inl_norm_rope_qk_fwd over the 24 q/k heads of the fused rows), as the
+        # encoder runners call it
+        lens = w.qwen3_op_lengths()
+        bats = w.batches(lens, 64)
+        c, s_ = inl_hip.rope_table(128, 1e6, 2048)
+        cos, sin = torch.from_numpy(c).to(dev), torch.from_numpy(s_).to(dev)
+        launches, nbytes = [], 0
+        for b in bats:
+            cu = w.cu_seqlens(b)
+            T = cu[-1]
+            qkv = torch.randn(T, 32, 128, generator=g, device=dev).to(torch.bfloat16)
+            rows = torch.from_numpy(inl_hip.positions(cu)).to(dev)
+            wq = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+            wk = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+            qko = torch.empty(T, 24, 128, device=dev, dtype=torch.bfloat16)
+            launches.append(lambda qkv=qkv, rows=rows, wq=wq, wk=wk, qko=qko: inl_hip.norm_rope_qk(
+                qkv[:, :24], 16, rows, cos, sin, q_weight=wq, k_weight=wk, eps=1e-6, out=qko, stream=stream))
+            # x read and y written (24 heads x 128 x 2 B each per token), the
+            # positions, both weights and the cos/sin rows of the longest text
+            nbytes += T * 24 * 128 * 2 * 2 + T * 4 + 2 * 128 * 2 + max(b) * 64 * 4 * 2
+        label = (f"config2 prologue, q and k in one launch per batch (inl_norm_rope_qk_fwd; Qwen3-0.6B: 16 q / 8 k "
+                 f"heads x 128, bf16 in/out, theta 1e6) over {sum(lens)} tokens in 12 batches")
         return label, "norm_rope_kernel<bf16, bf16>", len(launches), timed(launches), sum(lens), nbytes, "bf16"
     if name == "pool_last":
         # config 2 batches: final RMSNorm of each text's last row (hidden 1024,

@@ -454,6 +454,19 @@ extern "C" int inl_norm_rope_fwd(const inl_norm_rope_desc* d, const void* x, voi
   return inl::norm_rope_launch(d, x, y, weight, nullptr, 0, rows, cos, sin, cos2, sin2, stream);
 }
 
+extern "C" int inl_norm_rope_qk_fwd(const inl_norm_rope_desc* d, int32_t q_heads, const void* x, void* y,
+                                    const void* q_weight, const void* k_weight, const int32_t* rows,
+                                    const float* cos, const float* sin, const float* cos2, const float* sin2,
+                                    void* stream) {
+  using namespace inl;
+  if (!d) return fail(INL_E_INVALID, "norm_rope_qk: desc is NULL");
+  if (q_heads <= 0 || q_heads >= d->heads)
+    return fail(INL_E_INVALID, "norm_rope_qk: need 0 < q_heads < heads");
+  // heads >= q_heads take k_weight (ones when NULL: the kernel's default)
+  return norm_rope_launch_ex(d, x, y, q_weight, k_weight, q_heads, d->heads, d->heads, rows, cos, sin, cos2, sin2,
+                             stream);
+}
+
 extern "C" int inl_rope_table_host(int32_t rotary_dim, double theta, int32_t positions,
                                    int32_t mode, float* cos_out, float* sin_out) {
   using namespace inl;

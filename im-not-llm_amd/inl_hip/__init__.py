@@ -115,6 +115,8 @@ _kernel_name = _sig("inl_attn_kernel_name", ctypes.c_int, ctypes.POINTER(AttnDes
 
 _norm_rope = _sig("inl_norm_rope_fwd", ctypes.c_int, ctypes.POINTER(NormRopeDesc), c_void_p,
                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p)
+_norm_rope_qk = _sig("inl_norm_rope_qk_fwd", ctypes.c_int, ctypes.POINTER(NormRopeDesc), c_i32, c_void_p, c_void_p,
+                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p)
 _rope_table = _sig("inl_rope_table_host", ctypes.c_int, c_i32, ctypes.c_double, c_i32, c_i32,
                    c_void_p, c_void_p)
 _positions = _sig("inl_positions_host", ctypes.c_int, c_i32, c_void_p, c_void_p)
@@ -160,7 +162,8 @@ def exported_symbols() -> list:
     for n in ("inl_attn_plan_create", "inl_attn_plan_destroy", "inl_attn_plan_info",
               "inl_attn_fwd", "inl_attn_workspace_size", "inl_attn_varlen_fwd",
               "inl_attn_kernel_name",
-              "inl_norm_rope_fwd", "inl_rope_table_host", "inl_positions_host", "inl_pool_last_fwd",
+              "inl_norm_rope_fwd", "inl_norm_rope_qk_fwd", "inl_rope_table_host", "inl_positions_host",
+              "inl_pool_last_fwd",
               "inl_pool_mean_fwd", "inl_l2_normalize_fwd", "inl_pool_splade_fwd",
               "inl_last_error", "inl_abi_version"):
         if getattr(_lib, n, None) is not None:
@@ -447,6 +450,33 @@ def norm_rope(x, rows=None, cos=None, sin=None, *, weight=None, eps=1e-6, norm=T
     ptr = lambda t: t.data_ptr() if t is not None else None
     _check(_norm_rope(ctypes.byref(d), x.data_ptr(), out.data_ptr(), ptr(weight), ptr(rows),
                       ptr(cos), ptr(sin), ptr(cos2), ptr(sin2), _stream_ptr(stream)))
+    return out
+
+
+def norm_rope_qk(x, q_heads, rows=None, cos=None, sin=None, *, q_weight=None, k_weight=None, eps=1e-6,
+                 norm=True, rotary_dim=None, sections=1, cos2=None, sin2=None, out=None, out_dtype=None,
+                 round_tables=False, round_norm=False, stream=None):
+    """norm_rope over the q heads (``x[:, :q_heads]``, ``q_weight``) and k
+    heads (``x[:, q_heads:]``, ``k_weight``) of ``x [N, heads, head_dim]`` in
+    one launch (inl_norm_rope_qk_fwd)."""
+    import torch
+    n, heads, hd = x.shape
+    od = out_dtype if out_dtype is not None else x.dtype
+    if out is None:
+        out = torch.empty((n, heads, hd), dtype=od, device=x.device)
+    rd = (hd if cos is not None else 0) if rotary_dim is None else rotary_dim
+    d = NormRopeDesc()
+    d.n_tokens, d.heads, d.head_dim = n, heads, hd
+    d.x_row_stride, d.y_row_stride = x.stride(0), out.stride(0)
+    d.dtype, d.out_dtype = _dtype_code(x.dtype), _dtype_code(out.dtype)
+    d.norm, d.eps = int(bool(norm)), float(eps)
+    d.rotary_dim, d.sections = int(rd), int(sections)
+    d.table_rows = int(cos.shape[0]) if cos is not None else 0
+    d.round_tables, d.round_norm = int(bool(round_tables)), int(bool(round_norm))
+    ptr = lambda t: t.data_ptr() if t is not None else None
+    _check(_norm_rope_qk(ctypes.byref(d), int(q_heads), x.data_ptr(), out.data_ptr(), ptr(q_weight),
+                         ptr(k_weight), ptr(rows), ptr(cos), ptr(sin), ptr(cos2), ptr(sin2),
+                         _stream_ptr(stream)))
     return out
 
 

@@ -226,6 +226,20 @@ int inl_norm_rope_fwd(const inl_norm_rope_desc* desc, const void* x, void* y,
                       const float* cos, const float* sin,
                       const float* cos2, const float* sin2, void* stream);
 
+/* The q and k heads of one row in one launch: heads [0, q_heads) of each
+ * row are normalised with q_weight, heads [q_heads, desc->heads) with
+ * k_weight (NULL = all ones), every head rotated as inl_norm_rope_fwd does.
+ * For the q and k slices of a fused projection row (q heads then k heads,
+ * x_row_stride the fused row), the two per-tensor calls of the reference's
+ * attention prologue (qwen3/mod.rs:236-249: q_norm, k_norm, then rope of q
+ * and of k) become one launch over the same bytes. 0 < q_heads <
+ * desc->heads. Results equal two inl_norm_rope_fwd calls, bit for bit. */
+int inl_norm_rope_qk_fwd(const inl_norm_rope_desc* desc, int32_t q_heads,
+                         const void* x, void* y, const void* q_weight,
+                         const void* k_weight, const int32_t* rows,
+                         const float* cos, const float* sin,
+                         const float* cos2, const float* sin2, void* stream);
+
 /* Host helper: text-local positions of packed tokens (0..len-1 per text),
  * written to a host array of cu_seqlens_host[n_texts] entries. */
 int inl_positions_host(int32_t n_texts, const int32_t* cu_seqlens_host, int32_t* positions);

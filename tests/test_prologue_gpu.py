@@ -159,3 +159,39 @@ def test_strided_rows_in_place_and_bad_position(cuda, inl):
     ok = np.ones(n, bool)
     ok[5] = False
     assert np.abs(got[ok] - ref[ok]).max() <= 1e-5
+
+
+@pytest.mark.parametrize("case", ["qwen3", "gemma_bf16_rounding", "k_weightless"])
+def test_qk_one_launch_equals_two(case, cuda, inl):
+    """inl_norm_rope_qk_fwd over the q and k heads of fused projection rows
+    equals the two per-tensor launches bit for bit (the per-tensor path is
+    pinned to the oracle above); in place on the fused rows, the v columns
+    stay untouched; q_heads outside (0, heads) is refused."""
+    import torch
+    hq, hkv, d, theta, rnd = (16, 8, 128, 1e6, False) if case != "gemma_bf16_rounding" else (3, 1, 256, 1e4, True)
+    lens = [1, 37, 200, 5, 64]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    n = int(cu[-1])
+    g = torch.Generator(device=cuda).manual_seed(11)
+    qkv = (torch.randn(n, (hq + 2 * hkv) * d, generator=g, device=cuda) * 1.5).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(d, generator=g, device=cuda)).to(torch.bfloat16)
+    kw = None if case == "k_weightless" else (1 + 0.1 * torch.randn(d, generator=g, device=cuda)).to(torch.bfloat16)
+    rows = torch.from_numpy(inl.positions(cu)).to(cuda)
+    c, s = inl.rope_table(d, theta, max(lens))
+    cos, sin = torch.from_numpy(c).to(cuda), torch.from_numpy(s).to(cuda)
+    view = qkv.view(n, hq + 2 * hkv, d)
+    kw_ = dict(eps=1e-6, round_tables=rnd, round_norm=rnd)
+    print(f"case=norm_rope_qk {case} tokens={n}", flush=True)
+    qo = inl.norm_rope(view[:, :hq], rows, cos, sin, weight=qw, **kw_)
+    ko = inl.norm_rope(view[:, hq:hq + hkv], rows, cos, sin, weight=kw, **kw_)
+    both = inl.norm_rope_qk(view[:, :hq + hkv], hq, rows, cos, sin, q_weight=qw, k_weight=kw, **kw_)
+    torch.cuda.synchronize()
+    assert torch.equal(both[:, :hq], qo) and torch.equal(both[:, hq:], ko)
+    before = qkv.clone()
+    inl.norm_rope_qk(view[:, :hq + hkv], hq, rows, cos, sin, q_weight=qw, k_weight=kw, out=view[:, :hq + hkv], **kw_)
+    torch.cuda.synchronize()
+    assert torch.equal(view[:, :hq], qo) and torch.equal(view[:, hq:hq + hkv], ko)
+    assert torch.equal(qkv[:, (hq + hkv) * d:], before[:, (hq + hkv) * d:])
+    for bad in (0, hq + hkv):
+        with pytest.raises(inl.InlError):
+            inl.norm_rope_qk(view[:, :hq + hkv], bad, rows, cos, sin, q_weight=qw, k_weight=kw)
