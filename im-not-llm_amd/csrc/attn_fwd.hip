@@ -791,11 +791,16 @@ struct CostedItem {
 // workgroup of an XCD class a few percent above the class mean, because a
 // unit is large next to a workgroup's share (config 2: ~5.6 units per
 // workgroup, predicted maximum 1.035x the mean). Up to 32 times per class,
-// the most loaded workgroup gives one unit to, or trades one for a lighter
-// unit with, the workgroup of its class (among the 16 least loaded) that
-// lowers the pair's maximum the most (config 2: predicted 1.010x). Units
-// never leave their class, so the XCD placement of their K/V rows holds;
-// moved units run last in their new list.
+// the most loaded workgroup trades one unit for a lighter one of a workgroup
+// of its class (among the 16 least loaded), the trade that lowers the pair's
+// maximum the most (config 2: predicted 1.015x). A trade keeps both lists'
+// order, each unit taking the other's place, and is made only between units
+// whose start times overlap: the units after them shift by the difference of
+// the two weights alone, so every unit still runs beside the other q-blocks
+// of its text and finds their K/V rows in L2. (Moving units between lists
+// instead shifted whole list tails: 1.010x predicted, but 9-65 % more K/V
+// reads from L2 misses. The trades cost config 2 1.010x -> 1.036x the
+// algorithmic bytes for a 1.2 % faster step.)
 void rebalance(const std::vector<CostedItem>& items, int n_hg, int classes,
                std::vector<std::vector<int64_t>>* lists_p) {
   std::vector<std::vector<int64_t>>& lists = *lists_p;
@@ -810,7 +815,15 @@ void rebalance(const std::vector<CostedItem>& items, int n_hg, int classes,
       load[b] += wl[b].back();
     }
   }
-  std::vector<int64_t> wgs, dst_c;
+  auto starts = [&](int64_t b, std::vector<int64_t>* st) {
+    st->resize(wl[b].size());
+    int64_t acc = 0;
+    for (size_t k = 0; k < wl[b].size(); ++k) {
+      (*st)[k] = acc;
+      acc += wl[b][k];
+    }
+  };
+  std::vector<int64_t> wgs, dst_c, ss, sd;
   for (int c = 0; c < classes; ++c) {
     wgs.clear();
     int64_t total = 0;
@@ -832,48 +845,32 @@ void rebalance(const std::vector<CostedItem>& items, int n_hg, int classes,
                          [&](int64_t a, int64_t b) { return load[a] < load[b]; });
         dst_c.resize(16);
       }
+      starts(src, &ss);
       int64_t best = cur, bd = -1;
       size_t bi = 0, bj = 0;
-      bool bswap = false;
       const std::vector<int32_t>& ws = wl[src];
       for (int64_t d : dst_c) {
         if (d == src) continue;
         const int64_t ld = load[d];
         const std::vector<int32_t>& wdv = wl[d];
-        const bool room = (int64_t)wdv.size() < PP_MAX_UNITS;
+        starts(d, &sd);
         for (size_t i = 0; i < ws.size(); ++i) {
           const int64_t wa = ws[i];
-          if (room) {
-            const int64_t nm = std::max(cur - wa, ld + wa);
-            if (nm < best) { best = nm; bd = d; bi = i; bswap = false; }
-          }
           for (size_t j = 0; j < wdv.size(); ++j) {
             const int64_t diff = wa - wdv[j];
             if (diff <= 0) continue;
+            if (std::abs(ss[i] - sd[j]) > std::max<int64_t>(wa, wdv[j])) continue;
             const int64_t nm = std::max(cur - diff, ld + diff);
-            if (nm < best) { best = nm; bd = d; bi = i; bj = j; bswap = true; }
+            if (nm < best) { best = nm; bd = d; bi = i; bj = j; }
           }
         }
       }
       if (bd < 0) break;
-      const int64_t ua = lists[src][bi];
-      const int32_t wa = wl[src][bi];
-      lists[src].erase(lists[src].begin() + (std::ptrdiff_t)bi);
-      wl[src].erase(wl[src].begin() + (std::ptrdiff_t)bi);
-      load[src] -= wa;
-      if (bswap) {
-        const int64_t ub = lists[bd][bj];
-        const int32_t wb = wl[bd][bj];
-        lists[bd].erase(lists[bd].begin() + (std::ptrdiff_t)bj);
-        wl[bd].erase(wl[bd].begin() + (std::ptrdiff_t)bj);
-        load[bd] -= wb;
-        lists[src].push_back(ub);
-        wl[src].push_back(wb);
-        load[src] += wb;
-      }
-      lists[bd].push_back(ua);
-      wl[bd].push_back(wa);
-      load[bd] += wa;
+      std::swap(lists[src][bi], lists[bd][bj]);
+      const int64_t diff = (int64_t)wl[src][bi] - wl[bd][bj];
+      std::swap(wl[src][bi], wl[bd][bj]);
+      load[src] -= diff;
+      load[bd] += diff;
     }
   }
 }
@@ -1013,7 +1010,11 @@ void assign_units(const std::vector<CostedItem>& items, int n_hg, int gpk, Sched
       j0 = j1;
     }
   }
-  rebalance(items, n_hg, classes, &lists);
+  // Only with head-group affinity: under stream affinity (one K/V stream per
+  // XCD, long texts re-read in rounds) the trades cost more K/V traffic than
+  // they save time (EmbeddingGemma full attention: 1.1 % faster, 2.23x ->
+  // 2.62x the algorithmic bytes).
+  if (affinity) rebalance(items, n_hg, classes, &lists);
   s->items.reserve(U);
   s->unit_hg.reserve(U);
   // Without head-group affinity, equal-cost units (the q-blocks of one text,
