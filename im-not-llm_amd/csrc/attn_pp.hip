@@ -582,10 +582,12 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       }
     }
     ++t;
-    // Loads retire from vmcnt in issue order, stores independently of
-    // them: with at most 2 * KPW ops in flight, every load older than this
-    // phase's K/V loads (qn's loads among them) is done, whatever the
-    // stores do.
+    // With at most 2 * KPW ops in flight, every load older than this phase's
+    // K/V loads (qn's loads among them) is done: loads retire from vmcnt in
+    // issue order. (So do stores, in one order with the loads: the stores of
+    // this step's MFMA phase are done too.) This one asm statement is the
+    // only wait tied to qn: copies of qn that the compiler placed before
+    // it would read registers still in flight.
     static_assert(KST == 8, "the wait below names eight Q registers");
     asm volatile("s_waitcnt vmcnt(%8)"
                  : "+v"(qn[0]), "+v"(qn[1]), "+v"(qn[2]), "+v"(qn[3]), "+v"(qn[4]), "+v"(qn[5]),

@@ -512,9 +512,12 @@ __global__ __launch_bounds__(512, 1) void attn_pp64_kernel(AttnParams p) {
       }
     }
     ++t;
-    // Loads retire from vmcnt in issue order, stores independently of them:
-    // with at most 2 * KPW ops in flight, every load older than this phase's
-    // K/V loads (the Q loads among them) is done.
+    // With at most 2 * KPW ops in flight, every load older than this phase's
+    // K/V loads (the Q loads among them) is done: loads retire from vmcnt in
+    // issue order. (So do stores, in one order with the loads: the stores of
+    // this step's MFMA phase are done too.) This one asm statement is the
+    // only wait tied to qreg: copies of qreg that the compiler placed before
+    // it would read registers still in flight.
     static_assert(KST == 4, "the wait below names four Q registers");
     asm volatile("s_waitcnt vmcnt(%4)"
                  : "+v"(qreg[0]), "+v"(qreg[1]), "+v"(qreg[2]), "+v"(qreg[3])
