@@ -79,13 +79,15 @@ struct GemmShape {
   static_assert(NW % 2 == 0, "w blocks of one wave share its parity (GEGLU)");
   static_assert(STAGES >= 2 && (STAGES - 1) * PER_WAVE <= 63, "vmcnt range");
 };
-// 8 waves, 256 x 256 tiles, 3 stages, one workgroup per CU (128 KiB LDS);
-// 4 waves, 128 x 256 tiles, 2 stages, two workgroups per CU (64 KiB each), so
-// that one workgroup computes while the other drains its tile's stores.
-#ifndef INL_GEMM_SHAPE
-#define INL_GEMM_SHAPE 0
-#endif
-using GemmCfg = std::conditional_t<INL_GEMM_SHAPE == 1, GemmShape<4, 2, 2>, GemmShape<8, 3, 1>>;
+// Shape 0: 8 waves, 256 x 256 tiles, 3 stages, one workgroup per CU (128 KiB
+// LDS). Shape 1: 4 waves, 128 x 256 tiles, 2 stages, two workgroups per CU
+// (64 KiB each), so that one workgroup computes while the other drains its
+// tile's stores. Outputs of at most 256 columns (one n-tile per 256 rows of
+// x, whose rows then stream from HBM with no reuse) run on shape 1: at
+// 139,124 rows 7-8 % faster than shape 0, whose 544 tiles make 2.1 rounds
+// over 256 CUs; wider outputs run on shape 0 (shape 1 was 4-15 % slower).
+template <int SH>
+using GemmShapeOf = std::conditional_t<SH == 1, GemmShape<4, 2, 2>, GemmShape<8, 3, 1>>;
 
 enum GemmEpi { EPI_PLAIN = 0, EPI_GEGLU = 1, EPI_GELU_MUL = 2 };
 
@@ -113,9 +115,9 @@ __device__ __forceinline__ float gelu_tanh(float v) {
   return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
 }
 
-template <int EPI, bool OUT_BF16, bool ACC>
-__global__ __launch_bounds__(GemmCfg::NW * 64, GemmCfg::WPC) void gemm_bf16_kernel(GemmParams p) {
-  using C = GemmCfg;
+template <int SH, int EPI, bool OUT_BF16, bool ACC>
+__global__ __launch_bounds__(GemmShapeOf<SH>::NW * 64, GemmShapeOf<SH>::WPC) void gemm_bf16_kernel(GemmParams p) {
+  using C = GemmShapeOf<SH>;
   constexpr int GM_NW = C::NW, GM_BM = C::BM, GM_STAGES = C::STAGES, GM_STAGE = C::STAGE;
   constexpr int GM_PER_WAVE = C::PER_WAVE, GM_RING = C::RING;
   // output columns per tile: a GEGLU tile's 256 w rows are 128 gate + 128 up
@@ -393,9 +395,44 @@ __global__ __launch_bounds__(GemmCfg::NW * 64, GemmCfg::WPC) void gemm_bf16_kern
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the dummy loads past the end
 }
 
-template <int E, bool B, bool A>
+template <int SH, int E, bool B, bool A>
 const void* gemm_fn() {
-  return (const void*)gemm_bf16_kernel<E, B, A>;
+  return (const void*)gemm_bf16_kernel<SH, E, B, A>;
+}
+
+// The shape-dependent part of a launch: tile counts, workgroups and kernel.
+template <int SH>
+int gemm_launch_shape(GemmParams p, int epi, bool bf, bool acc, int64_t m, int64_t k, int cus, void* stream) {
+  using C = GemmShapeOf<SH>;
+  p.n_tiles = ((m + C::BM - 1) / C::BM) * p.n_tiles_n;
+  p.per_xcd = (p.n_tiles + GM_XCDS - 1) / GM_XCDS;
+  // C::WPC workgroups per CU, at most one per tile of an XCD's range
+  const int64_t per_xcd_wg = std::max<int64_t>(1, std::min<int64_t>(cus / GM_XCDS * C::WPC, p.per_xcd));
+  p.wg_per_xcd = (int32_t)per_xcd_wg;
+  if ((int64_t)(p.per_xcd + per_xcd_wg - 1) / per_xcd_wg * (k / GM_BK) >= ((int64_t)1 << 31))
+    return fail(INL_E_UNSUPPORTED, "gemm: too many k stages per workgroup");
+  const void* fn = nullptr;
+  switch (epi * 4 + (bf ? 2 : 0) + (acc ? 1 : 0)) {
+#define INL_GEMM_CASE(E, B, A) \
+  case E * 4 + (B ? 2 : 0) + (A ? 1 : 0): fn = gemm_fn<SH, E, B, A>(); break;
+    INL_GEMM_CASE(EPI_PLAIN, false, false)
+    INL_GEMM_CASE(EPI_PLAIN, false, true)
+    INL_GEMM_CASE(EPI_PLAIN, true, false)
+    INL_GEMM_CASE(EPI_PLAIN, true, true)
+    INL_GEMM_CASE(EPI_GEGLU, false, false)
+    INL_GEMM_CASE(EPI_GEGLU, true, false)
+    INL_GEMM_CASE(EPI_GELU_MUL, false, false)
+    INL_GEMM_CASE(EPI_GELU_MUL, true, false)
+#undef INL_GEMM_CASE
+    default:
+      return fail(INL_E_UNSUPPORTED, "gemm: the gated epilogues take beta = 0");
+  }
+  int rc = set_max_dynamic_lds(fn, C::LDS);
+  if (rc) return rc;
+  void* args[] = {&p};
+  INL_HIP_TRY(hipLaunchKernel(fn, dim3((unsigned)(per_xcd_wg * GM_XCDS)), dim3(C::NW * 64), args, C::LDS,
+                              (hipStream_t)stream));
+  return INL_OK;
 }
 
 // Launch for every epilogue; `n` is the output width (GEGLU: w has 2n rows).
@@ -418,7 +455,7 @@ int gemm_launch(int epi, int64_t m, int64_t n, int64_t k, const void* x, int64_t
   if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)y & 15) || ((uintptr_t)mul & 7))
     return fail(INL_E_INVALID, "gemm: x, w and y must be 16-byte aligned, the multiplier 8-byte aligned");
   // each tile's descriptor spans at most 256 rows of x or w
-  if ((int64_t)GemmCfg::BM * xs * 2 >= ((int64_t)1 << 32) || (int64_t)GM_BN * ws * 2 >= ((int64_t)1 << 32))
+  if ((int64_t)256 * xs * 2 >= ((int64_t)1 << 32) || (int64_t)GM_BN * ws * 2 >= ((int64_t)1 << 32))
     return fail(INL_E_UNSUPPORTED, "gemm: row strides too large for a tile's 32-bit buffer range");
   int dev = 0, cus = 0;
   INL_HIP_TRY(hipGetDevice(&dev));
@@ -439,36 +476,9 @@ int gemm_launch(int epi, int64_t m, int64_t n, int64_t k, const void* x, int64_t
   p.alpha = alpha;
   p.beta = beta;
   p.n_tiles_n = (int32_t)((n + bno - 1) / bno);
-  p.n_tiles = ((m + GemmCfg::BM - 1) / GemmCfg::BM) * p.n_tiles_n;
-  p.per_xcd = (p.n_tiles + GM_XCDS - 1) / GM_XCDS;
-  // GemmCfg::WPC workgroups per CU, at most one per tile of an XCD's range
-  const int64_t per_xcd_wg = std::max<int64_t>(1, std::min<int64_t>(cus / GM_XCDS * GemmCfg::WPC, p.per_xcd));
-  p.wg_per_xcd = (int32_t)per_xcd_wg;
-  if ((int64_t)(p.per_xcd + per_xcd_wg - 1) / per_xcd_wg * (k / GM_BK) >= ((int64_t)1 << 31))
-    return fail(INL_E_UNSUPPORTED, "gemm: too many k stages per workgroup");
   const bool bf = out_dtype == INL_BF16, acc = beta != 0.f;
-  const void* fn = nullptr;
-  switch (epi * 4 + (bf ? 2 : 0) + (acc ? 1 : 0)) {
-#define INL_GEMM_CASE(E, B, A) \
-  case E * 4 + (B ? 2 : 0) + (A ? 1 : 0): fn = gemm_fn<E, B, A>(); break;
-    INL_GEMM_CASE(EPI_PLAIN, false, false)
-    INL_GEMM_CASE(EPI_PLAIN, false, true)
-    INL_GEMM_CASE(EPI_PLAIN, true, false)
-    INL_GEMM_CASE(EPI_PLAIN, true, true)
-    INL_GEMM_CASE(EPI_GEGLU, false, false)
-    INL_GEMM_CASE(EPI_GEGLU, true, false)
-    INL_GEMM_CASE(EPI_GELU_MUL, false, false)
-    INL_GEMM_CASE(EPI_GELU_MUL, true, false)
-#undef INL_GEMM_CASE
-    default:
-      return fail(INL_E_UNSUPPORTED, "gemm: the gated epilogues take beta = 0");
-  }
-  int rc = set_max_dynamic_lds(fn, GemmCfg::LDS);
-  if (rc) return rc;
-  void* args[] = {&p};
-  INL_HIP_TRY(hipLaunchKernel(fn, dim3((unsigned)(per_xcd_wg * GM_XCDS)), dim3(GemmCfg::NW * 64), args, GemmCfg::LDS,
-                              (hipStream_t)stream));
-  return INL_OK;
+  if (p.n_tiles_n == 1) return gemm_launch_shape<1>(p, epi, bf, acc, m, k, cus, stream);
+  return gemm_launch_shape<0>(p, epi, bf, acc, m, k, cus, stream);
 }
 
 }  // namespace

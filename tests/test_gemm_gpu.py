@@ -45,17 +45,19 @@ def test_gemm_against_fp32(m, n, k, out, cuda, inl):
         assert (err <= 2.0 ** -8 * ref.abs() + 1e-5 * scale).all()
 
 
-def test_gemm_strides_alpha_beta(cuda, inl):
+@pytest.mark.parametrize("n", [512, 200])
+def test_gemm_strides_alpha_beta(n, cuda, inl):
     """Strided x, w and y rows (q/k/v-style slices of wider rows), alpha, and
     beta = 1 accumulation into f32 and into bf16 outputs; columns of y outside
-    [0, n) are left untouched."""
+    [0, n) are left untouched. n = 200 is one n-tile (the 128-row kernel
+    shape), n = 512 two (the 256-row shape)."""
     import torch
-    m, n, k = 700, 512, 256
+    m, k = 700, 256
     xs = _rand(torch, cuda, (m, k + 72), 3)
     ws = _rand(torch, cuda, (n, k + 40), 4, k ** -0.5)
     x, w = xs[:, 8:8 + k], ws[:, :k]
     ref = x.double() @ w.double().T
-    print("case=gemm strides alpha beta", flush=True)
+    print(f"case=gemm strides alpha beta n={n}", flush=True)
     for od in (torch.float32, torch.bfloat16):
         base = torch.randn(m, n + 24, device=cuda).to(od)
         y = base.clone()
@@ -134,8 +136,9 @@ def _gelu_tanh(v):
     return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v ** 3)))
 
 
-@pytest.mark.parametrize("mode,m,n,k", [("geglu", 300, 200, 64), ("geglu", 3001, 1152, 768),
-                                        ("gelu_mul", 257, 264, 96), ("gelu_mul", 3001, 256, 768)])
+@pytest.mark.parametrize("mode,m,n,k", [("geglu", 300, 200, 64), ("geglu", 3001, 1152, 768), ("geglu", 517, 96, 128),
+                                        ("gelu_mul", 257, 264, 96), ("gelu_mul", 3001, 256, 768),
+                                        ("gelu_mul", 130, 72, 64)])
 def test_gated_gemm_against_fp64(mode, m, n, k, cuda, inl):
     """The fused GEGLU and GELU x multiplier epilogues against the f64
     product of the same bf16 values, gelu_tanh in f64: within the bf16
