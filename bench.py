@@ -154,7 +154,58 @@ def cpu_baseline(batches, inputs, hq, hkv, d, causal, window, scale, seconds):
                    f"online-softmax attention as candle's CPU flash path, 64-key blocks, 8-wide AVX2 dot "
                    f"products, OpenMP over (text, head, 16-row block)), {spent:.2f} s"),
         "tflops": round(flops / spent / 1e12, 4),
+        "cross_check": torch_cpu_sdpa(batches, host, hq, hkv, causal, window, scale, min(3.0, seconds / 4)),
     }
+
+
+def torch_cpu_sdpa(batches, host, hq, hkv, causal, window, scale, seconds):
+    """A sanity cross-check beside the CPU baseline, not the baseline: torch's
+    CPU scaled_dot_product_attention in f32, one call per text (GQA through
+    enable_gqa, the window as a boolean mask), over the workload's batches in
+    order until `seconds` of work. Its first batch is compared with the
+    oracle's C restatement on the same inputs."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    from oracle import cref, attention as oa
+
+    def run(i):
+        qh, kh, vh = host[i]
+        cu = oa.cu_from_lengths(batches[i])
+        out = np.empty_like(qh)
+        for a, b in zip(cu[:-1], cu[1:]):
+            q = torch.from_numpy(qh[a:b]).transpose(0, 1).unsqueeze(0)
+            k = torch.from_numpy(kh[a:b]).transpose(0, 1).unsqueeze(0)
+            v = torch.from_numpy(vh[a:b]).transpose(0, 1).unsqueeze(0)
+            mask = None
+            if window >= 0:
+                r = torch.arange(b - a)
+                mask = (r[None, :] - r[:, None]).abs() <= window
+                if causal:
+                    mask &= r[None, :] <= r[:, None]
+            o = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=causal and mask is None,
+                                               scale=scale, enable_gqa=hq != hkv)
+            out[a:b] = o[0].transpose(0, 1).numpy()
+        return out
+
+    with torch.inference_mode():
+        first = run(0)
+        qh, kh, vh = host[0]
+        ref = cref.attention_f32(qh, kh, vh, oa.cu_from_lengths(batches[0]), causal=causal, window=window,
+                                 scale=scale)
+        diff = float(np.abs(first - ref).max())
+        tokens, spent, used = 0, 0.0, 0
+        while spent < seconds:
+            i = used % len(batches)
+            t0 = time.perf_counter()
+            run(i)
+            spent += time.perf_counter() - t0
+            tokens += int(sum(batches[i]))
+            used += 1
+    return {"what": "torch CPU scaled_dot_product_attention, f32, per text (a cross-check, not the baseline)",
+            "value": round(tokens / spent, 1), "unit": "tokens/s", "threads": torch.get_num_threads(),
+            "sample": f"{used} batch launches, {tokens} tokens, {spent:.2f} s",
+            "max_abs_diff_vs_port": diff}
 
 
 def read_traffic(name: str):
@@ -236,7 +287,12 @@ def e2e_cpu_baseline(weights, shape, ids, cu, seconds):
     return {"value": round(tokens / spent, 1), "unit": "tokens/s", "cores": int(cores), "kind": "port",
             "cpu_model": cpu_model(),
             "sample": (f"{runs} encodes of the same {len(cu) - 1} texts ({int(cu[-1])} tokens each) through "
-                       f"oracle/qwen3.py (numpy f32 forward: BLAS GEMMs, per-text attention), {spent:.2f} s")}
+                       f"oracle/qwen3.py (numpy f32 forward: BLAS GEMMs, per-text attention), {spent:.2f} s"),
+            "reference_published": {"value": 178, "unit": "tokens/s",
+                                    "what": ("the reference's own CPU f32 figure for Qwen3-Embedding-0.6B at "
+                                             "batch 8 on a Ryzen 5 3600 (6 cores; other hardware, real "
+                                             "checkpoint and text)"),
+                                    "source": "docs/DEVICES.md:429"}}
 
 
 def qwen3_e2e_measure(torch, inl_hip, dev, bf16, steps, warmup, cpu_seconds, no_cpu):
@@ -386,7 +442,12 @@ def gemma_e2e_cpu_baseline(host_w, tc, seconds):
     return {"value": round(tokens / spent, 1), "unit": "tokens/s", "cores": int(cores), "kind": "port",
             "cpu_model": cpu_model(),
             "sample": (f"{runs} encodes of 4 texts U[64,512] ({int(cu[-1])} tokens each) through oracle/gemma2.py "
-                       f"(numpy f32 forward: BLAS GEMMs, per-text attention) with the same weights, {spent:.2f} s")}
+                       f"(numpy f32 forward: BLAS GEMMs, per-text attention) with the same weights, {spent:.2f} s"),
+            "reference_published": {"value": 424, "unit": "tokens/s",
+                                    "what": ("the reference's own CPU f32 figure for EmbeddingGemma 2 at batch 8 "
+                                             "on a Ryzen 5 3600 (6 cores; other hardware, real checkpoint and "
+                                             "text)"),
+                                    "source": "docs/DEVICES.md:430"}}
 
 
 def gemma_e2e_main(args):
