@@ -53,6 +53,12 @@ EXTRA = {
 # the compiler's resource-usage remarks and fails if any of them does.
 NO_SCRATCH = {"attn_pp.hip", "attn_pp64.hip", "attn_wide.hip", "gemm.hip", "splade_decoder.hip"}
 RESOURCE_REMARKS = ["-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"]
+# The same sources are also compiled to a device assembly listing, which
+# asmcheck.py walks for instructions that name a register an inline-asm
+# load has not yet written (a copy placed before the load's wait). These
+# have register-writing asm loads; the check must find some there, so that a
+# listing format the parser no longer reads cannot pass silently.
+ASM_REGISTER_LOADS = {"attn_pp.hip", "attn_pp64.hip", "attn_wide.hip"}
 
 
 def scratch_users(remarks: str) -> list[str]:
@@ -94,6 +100,25 @@ def check_no_scratch(src_name: str, remarks: str) -> None:
         raise RuntimeError(f"{src_name}: kernels with inline-asm loads use scratch: " + ", ".join(users))
 
 
+def check_inflight(src_name: str, listing: str) -> None:
+    """Raise if the device listing of a source with inline-asm loads names a
+    register before the wait that retires its load (see asmcheck.py)."""
+    sys.path.insert(0, str(PKG))
+    try:
+        import asmcheck
+    finally:
+        sys.path.pop(0)
+    loads = asmcheck.count_asm_loads(listing)
+    if src_name in ASM_REGISTER_LOADS and loads == 0:
+        raise RuntimeError(f"{src_name}: no register-writing inline-asm loads found in its listing, so the "
+                           "in-flight register check cannot be made")
+    bad = asmcheck.check_listing(listing)
+    if bad:
+        shown = "\n".join(str(v) for v in bad[:10])
+        raise RuntimeError(f"{src_name}: {len(bad)} instructions name registers whose inline-asm loads are "
+                           f"still in flight:\n{shown}")
+
+
 def sources():
     return sorted(CSRC.glob("*.hip"))
 
@@ -111,14 +136,18 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     tmp = OUT.with_suffix(".so.tmp")
     with tempfile.TemporaryDirectory(prefix="inl_hip_build_") as objdir:
-        jobs = []
+        jobs, listings = [], []
         for src in sources():
             obj = Path(objdir) / (src.stem + ".o")
             cmd = [HIPCC, *FLAGS, "-c", *EXTRA.get(src.name, []),
                    *(RESOURCE_REMARKS if src.name in NO_SCRATCH else []), str(src), "-o", str(obj)]
             jobs.append((src, obj, cmd))
+            if src.name in NO_SCRATCH:
+                lst = Path(objdir) / (src.stem + ".s")
+                listings.append((src, lst, [HIPCC, *FLAGS, "-S", "--cuda-device-only", *EXTRA.get(src.name, []),
+                                            str(src), "-o", str(lst)]))
         with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1, 8)) as pool:
-            results = list(pool.map(lambda j: _run(j[2]), jobs))
+            results = list(pool.map(lambda j: _run(j[2]), jobs + listings))
         for (src, _, _), (rc, err) in zip(jobs, results):
             if rc != 0:
                 raise RuntimeError(f"hipcc failed on {src.name} ({rc}):\n{err}")
@@ -127,6 +156,10 @@ def build(verbose: bool = False) -> Path:
                 err = "\n".join(l for l in err.splitlines() if "kernel-resource-usage" not in l)
             if verbose and err.strip():
                 print(err, file=sys.stderr)
+        for (src, lst, _), (rc, err) in zip(listings, results[len(jobs):]):
+            if rc != 0:
+                raise RuntimeError(f"hipcc -S failed on {src.name} ({rc}):\n{err}")
+            check_inflight(src.name, lst.read_text())
         rc, err = _run([HIPCC, *LINK_FLAGS, *(str(o) for _, o, _ in jobs), "-o", str(tmp)])
         if rc != 0:
             raise RuntimeError(f"hipcc link failed ({rc}):\n{err}")

@@ -246,6 +246,74 @@ def test_no_scratch_remarks_are_parsed_from_a_real_compile(tmp_path):
     b.check_no_scratch(src.name, r.stderr)
 
 
+def _asmcheck():
+    import importlib.util
+    import sys
+    spec = importlib.util.spec_from_file_location("inl_asmcheck", ROOT / "im-not-llm_amd" / "asmcheck.py")
+    m = importlib.util.module_from_spec(spec)
+    sys.modules[spec.name] = m   # dataclasses look their module up there
+    spec.loader.exec_module(m)
+    return m
+
+
+def _listing(body):
+    return "\t.globl\tk\nk:\n" + "\n".join("\t" + l if not l.endswith(":") else l for l in body) + "\n.Lfunc_end0:\n"
+
+
+def test_inflight_register_check_on_listings():
+    """The build walks the device listing of every kernel with inline-asm
+    loads for instructions that name a register whose load is still in
+    flight (the compiler treats the asm output as written when the asm
+    statement ends). A copy before the wait is caught, on any path of the
+    control flow; a wait that has enough younger memory operations behind it
+    retires the load; direct-to-LDS loads write no register."""
+    ac = _asmcheck()
+    load = [";;#ASMSTART", "buffer_load_dwordx4 v[4:7], v1, s[0:3], 0 offen offset:32", ";;#ASMEND"]
+    dma = [";;#ASMSTART", "buffer_load_dwordx4 v2, s[0:3], 0 offen lds", ";;#ASMEND"]
+    copy = ["v_mov_b64_e32 v[8:9], v[6:7]"]
+    end = ["s_endpgm"]
+    bad = ac.check_listing(_listing(load + copy + ["s_waitcnt vmcnt(0)"] + end))
+    assert len(bad) == 1 and bad[0].registers == ["v6", "v7"], bad
+    assert ac.check_listing(_listing(load + ["s_waitcnt vmcnt(0)"] + copy + end)) == []
+    # vmcnt(1) retires the load only with one younger memory operation
+    assert ac.check_listing(_listing(load + dma + ["s_waitcnt vmcnt(1)"] + copy + end)) == []
+    assert len(ac.check_listing(_listing(load + ["s_waitcnt vmcnt(1)"] + copy + end))) == 1
+    # the register-writing load of a wait-free branch reaches the copy at the join
+    branchy = load + ["s_cbranch_scc1 .LBB0_2", "s_waitcnt vmcnt(0)", "s_branch .LBB0_3", ".LBB0_2:",
+                      "s_nop 0", ".LBB0_3:"] + copy + end
+    assert len(ac.check_listing(_listing(branchy))) == 1
+    both = load + ["s_cbranch_scc1 .LBB0_2", "s_waitcnt vmcnt(0)", "s_branch .LBB0_3", ".LBB0_2:",
+                   "s_waitcnt vmcnt(0)", ".LBB0_3:"] + copy + end
+    assert ac.check_listing(_listing(both)) == []
+    # a loop: the load at the bottom reaches the copy at the top on the next
+    # turn, and the load itself then writes registers still in flight
+    loop = [".LBB0_1:"] + copy + load + ["s_cbranch_scc1 .LBB0_1", "s_waitcnt vmcnt(0)"] + end
+    assert [v.text.split()[0] for v in ac.check_listing(_listing(loop))] == ["v_mov_b64_e32", "buffer_load_dwordx4"]
+    assert ac.count_asm_loads(_listing(load + dma + end)) == 1
+
+
+def test_inflight_register_check_on_a_real_listing(tmp_path):
+    """attn_pp64's listing, compiled with the build's flags, holds its
+    register-writing asm loads (the next unit's Q) and names none of their
+    registers before the wait that retires them."""
+    import importlib.util
+    import subprocess
+    spec = importlib.util.spec_from_file_location("inl_build", ROOT / "im-not-llm_amd" / "build.py")
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    src = ROOT / "im-not-llm_amd" / "csrc" / "attn_pp64.hip"
+    assert src.name in b.ASM_REGISTER_LOADS <= b.NO_SCRATCH
+    out = tmp_path / "pp64.s"
+    r = subprocess.run([b.HIPCC, *b.FLAGS, "-S", "--cuda-device-only", str(src), "-o", str(out)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    ac = _asmcheck()
+    text = out.read_text()
+    assert ac.count_asm_loads(text) > 0
+    assert ac.check_listing(text) == []
+    b.check_inflight(src.name, text)
+
+
 def test_small_f32_batches_split_their_key_ranges():
     """f32 batches too small to fill the GPU get a key-range split (partial
     outputs in the plan's memory, so a larger workspace); bf16 descs, large
