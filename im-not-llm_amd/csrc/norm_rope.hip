@@ -160,7 +160,7 @@ __device__ __forceinline__ void xor_lanes8(const float (&in)[8], float (&out)[8]
 }
 // A group of G = head_dim / 8 lanes owns one token: each lane holds 8
 // elements of a head row. The token's norm weights, table row and the lane's
-// cos/sin columns are loaded once per group of HB (4 or 8) heads of the token
+// cos/sin columns are loaded once per group of HB (4, 5 or 8) heads of the token
 // (each lane group owns one (token, head chunk)), so per (token, head) x is
 // read and y written and the tables cost 1/HB of that in cache reads; the
 // HB loads of a lane go out together. Heads [0, w2_heads) take weight w,
@@ -400,8 +400,10 @@ int norm_rope_launch_ex(const inl_norm_rope_desc* d, const void* x, void* y, con
 
   const int G = hd >> 3;
   // heads per lane group: 8 for 5-7 heads (a fused q/k/v row: one group per
-  // token), else 4 (8 was slower on 8 and 16 heads of head_dim 128)
-  const int HB = d->heads > 4 && d->heads < 8 ? 8 : 4;
+  // token), else 4 (8 was slower on 8 and 16 heads of head_dim 128). The
+  // fused row of EmbeddingGemma (3 q + 1 k + 1 v heads of 256) takes exactly
+  // 5: no repeated loads of its last head, and 16 fewer registers.
+  const int HB = d->heads == 5 && G == 32 ? 5 : (d->heads > 4 && d->heads < 8 ? 8 : 4);
   const int64_t groups_per_block = 256 / G;
   const int64_t groups = d->n_tokens * ((d->heads + HB - 1) / HB);   // (token, HB-head chunk)
   if (groups + groups_per_block >= ((int64_t)1 << 31))
@@ -424,7 +426,8 @@ int norm_rope_launch_ex(const inl_norm_rope_desc* d, const void* x, void* y, con
         default: hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 64, H>), grid, block, 0, st, p);
       }
     };
-    if (HB == 8) go(std::integral_constant<int, 8>{});
+    if (HB == 5) hipLaunchKernelGGL((norm_rope_kernel<TI, TO, 32, 5>), grid, block, 0, st, p);
+    else if (HB == 8) go(std::integral_constant<int, 8>{});
     else go(std::integral_constant<int, 4>{});
   };
   if (d->dtype == INL_BF16 && d->out_dtype == INL_BF16) launch(bf16{}, bf16{});
