@@ -373,10 +373,14 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
           __builtin_amdgcn_raw_buffer_store_b128(val, ors, o_off + (db * 32 + 8 * g) * 4, 0, 2);
         }
     }
+    // Zero the accumulators on the matrix core, idle during the store:
+    // 0 * 0 + 0 per element, one instruction per 16 registers.
+    f16x8 z = {};
 #pragma unroll
-    for (int i = 0; i < NDB; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[i][r] = 0.f;
+    for (int i = 0; i < NDB; ++i) {
+      asm volatile("" : "+v"(z));   // one opaque operand per product, so none is merged with another
+      oacc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(z, z, (f32x16){}, 0, 0, 0);
+    }
     m_i = -INFINITY;
     l_i = 0.f;
   };
@@ -437,19 +441,25 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
     if (__builtin_expect(__builtin_amdgcn_ballot_w64(mx > m_i + 8.0f) != 0, 0)) {
       const float m_new = __builtin_elementwise_maximum(m_i, mx);
       const float alpha = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_new);
+      // A row whose m_i is -inf has accumulated nothing (its O^T is zero), so
+      // when no row has, scaling by alpha = 0 would change nothing: the first
+      // tile of every unit skips it.
+      const bool fresh = __builtin_amdgcn_ballot_w64(m_i != -INFINITY) == 0;
       m_i = m_new;
       l_i *= alpha;
       // O^T lives in AGPRs (the PV MFMAs' accumulators); the products go
       // back there explicitly, so that the paths with and without this
       // rescale meet in AGPRs instead of copying O^T through VGPRs.
+      if (!fresh) {
 #pragma unroll
-      for (int i = 0; i < NDB; ++i)
+        for (int i = 0; i < NDB; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float y;
-          asm("v_accvgpr_write_b32 %0, %1" : "=a"(y) : "v"(oacc[i][r] * alpha));
-          oacc[i][r] = y;
-        }
+          for (int r = 0; r < 16; ++r) {
+            float y;
+            asm("v_accvgpr_write_b32 %0, %1" : "=a"(y) : "v"(oacc[i][r] * alpha));
+            oacc[i][r] = y;
+          }
+      }
     }
     // Three MFMA groups, each with VALU and LDS work in its shadow:
     //   QK^T of tile j + 1 (16)   P of k-step 0, its V fragments, K reads
