@@ -818,6 +818,41 @@ def op_main(args):
     }), flush=True)
 
 
+def stream_reference():
+    """HBM bandwidth that torch's own streaming kernels reach (HIP events, 20
+    launches each after 3 warm-up launches): the practical ceiling next to
+    the 8 TB/s peak that the HBM-bound rows are measured against. Sizes of
+    1 GiB and more keep the data out of the 256 MB last-level cache."""
+    import torch
+    dev = torch.device("cuda:0")
+    out = {"what": "torch streaming kernels, f32, bytes moved per launch / launch time", "unit": "TB/s"}
+    for gib in (1, 4):
+        n = gib * (1 << 30) // 4
+        x = torch.randn(n, device=dev)
+        y = torch.randn(n, device=dev)
+
+        def rate(f, nbytes):
+            for _ in range(3):
+                f()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(20):
+                f()
+            b.record()
+            torch.cuda.synchronize()
+            return round(nbytes / (a.elapsed_time(b) / 20 * 1e-3) / 1e12, 2)
+
+        out[f"{gib}_GiB"] = {
+            "copy (1 read + 1 write)": rate(lambda: y.copy_(x), 2 * n * 4),
+            "add in place (2 reads + 1 write)": rate(lambda: y.add_(x), 3 * n * 4),
+            "fill (1 write)": rate(lambda: y.fill_(0.5), n * 4),
+            "sum (1 read)": rate(lambda: torch.sum(x), n * 4),
+        }
+        del x, y
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -831,7 +866,14 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (3 launches): the known-size "
                          "reference that scales the FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--stream-reference", action="store_true",
+                    help="only time torch's own streaming kernels (copy, in-place add, fill, sum) over 1 and "
+                         "4 GiB: what a plain element-wise kernel reaches on this GPU's HBM")
     args = ap.parse_args()
+
+    if args.stream_reference:
+        stream_reference()
+        return
 
     if args.copy_calibration:
         import torch
