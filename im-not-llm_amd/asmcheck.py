@@ -14,8 +14,10 @@ once made a kernel compute with a stale Q operand.)
 propagates the set of in-flight registers along it, with the number of
 vector-memory instructions issued since each one's load (the minimum over
 the paths that reach a point). Any instruction other than a wait that names
-an in-flight register is reported. Direct-to-LDS loads (``... lds``) write no
-register and are only counted.
+an in-flight register is reported, except as the destination of another
+load: loads write their registers in issue order, so the younger load's
+value is the one that stays (its address operands are still checked).
+Direct-to-LDS loads (``... lds``) write no register and are only counted.
 """
 from __future__ import annotations
 
@@ -164,10 +166,16 @@ def _transfer(insts, state, function, report):
         is_vmem = bool(_VMEM.match(inst.mnemonic))
         named = _regs(inst.operands)
         writes = set()
-        if inst.in_asm and is_vmem and _VMEM_LOAD.match(inst.mnemonic) and not inst.operands.rstrip().endswith("lds") \
-                and " lds" not in f" {inst.operands} ":
-            first = inst.operands.split(",", 1)[0]
-            writes = _regs(first)
+        reg_load = is_vmem and bool(_VMEM_LOAD.match(inst.mnemonic)) and " lds" not in f" {inst.operands} "
+        if reg_load:
+            # A load's destination may be a register still in flight from an
+            # older load: loads retire, and write their registers, in issue
+            # order, so the younger value lands last. Its address operands
+            # are still checked.
+            dest = _regs(inst.operands.split(",", 1)[0])
+            named = named - dest
+            if inst.in_asm:
+                writes = dest
         hit = sorted((named & st.keys()), key=lambda r: (r[0], int(r[1:])))
         if hit and report is not None:
             report.append(Violation(function, inst.line, inst.text, hit))

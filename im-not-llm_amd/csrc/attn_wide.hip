@@ -539,19 +539,22 @@ __global__ __launch_bounds__(256, 1) void attn_wide_kernel(AttnParams p) {
     // retires the loads issued before it, not this step's), then the loads
     // of tile j + 3: issued at the end of the step, they run faster than
     // anywhere earlier, where they share LDS with the fragment reads.
-    if (__builtin_expect(qt + 1 == qhi && qu + 1 < nu, 0)) load_q_of(qu + 1);
+    // The QK cursor moves to tile j + 2, into the next unit (whose Q^T is
+    // loaded now) when tile j + 1 ended its unit: one test for both.
+    if (__builtin_expect(++qt == qhi, 0)) {
+      if (qu + 1 < nu) load_q_of(qu + 1);
+      if (++qu < nu) {
+        int a, b, c, lo, hi, d;
+        unit(qu, a, b, c, lo, hi, d);
+        qt = lo;
+        qhi = hi;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < DMA_PARTS; ++i) dma_part(i, st_dma);
     __builtin_amdgcn_sched_barrier(0);
     l_i += lsum[0];
     dma_advance();
-    // the QK cursor moves to tile j + 2
-    if (__builtin_expect(++qt == qhi, 0) && ++qu < nu) {
-      int a, b, c, lo, hi, d;
-      unit(qu, a, b, c, lo, hi, d);
-      qt = lo;
-      qhi = hi;
-    }
     // the softmax / PV cursor moves to tile j + 1
     if (__builtin_expect(t + 1 == hi_t, 0)) {
       capture_out();

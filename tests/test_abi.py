@@ -286,9 +286,17 @@ def test_inflight_register_check_on_listings():
                    "s_waitcnt vmcnt(0)", ".LBB0_3:"] + copy + end
     assert ac.check_listing(_listing(both)) == []
     # a loop: the load at the bottom reaches the copy at the top on the next
-    # turn, and the load itself then writes registers still in flight
+    # turn; the load itself may write registers still in flight from its
+    # previous turn (loads write in issue order, the younger value stays)
     loop = [".LBB0_1:"] + copy + load + ["s_cbranch_scc1 .LBB0_1", "s_waitcnt vmcnt(0)"] + end
-    assert [v.text.split()[0] for v in ac.check_listing(_listing(loop))] == ["v_mov_b64_e32", "buffer_load_dwordx4"]
+    assert [v.text.split()[0] for v in ac.check_listing(_listing(loop))] == ["v_mov_b64_e32"]
+    assert ac.check_listing(_listing(load + load + ["s_waitcnt vmcnt(0)"] + copy + end)) == []
+    # ... but not a VALU write into them, nor an address taken from them
+    overwrite = ["v_mov_b32_e32 v5, 0"]
+    assert len(ac.check_listing(_listing(load + overwrite + ["s_waitcnt vmcnt(0)"] + end))) == 1
+    addr = [";;#ASMSTART", "buffer_load_dwordx4 v[8:11], v5, s[0:3], 0 offen", ";;#ASMEND"]
+    bad = ac.check_listing(_listing(load + addr + ["s_waitcnt vmcnt(0)"] + end))
+    assert len(bad) == 1 and bad[0].registers == ["v5"], bad
     assert ac.count_asm_loads(_listing(load + dma + end)) == 1
 
 
