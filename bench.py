@@ -43,7 +43,9 @@ on the library's own bf16 kernel); its CPU leg also checks three of the
 timed batch's texts against the oracle. The default line nests the
 configuration-1 end-to-end measurement (f32, a new 8-text draw every step)
 under `e2e_config1`; --workload gemm times one configuration-3 layer's GEMMs
-on the library's bf16 kernel.
+on the library's bf16 kernel. --stream-reference times torch's own streaming
+kernels (copy, in-place add, fill, sum over 1 and 4 GiB): what a plain
+element-wise kernel reaches on the GPU's HBM, next to the 8 TB/s peak.
 """
 from __future__ import annotations
 
